@@ -1,0 +1,262 @@
+"""Benchmark: fwd+bwd atoms/sec of cufk_amd.reconstruct at B=4096, N=2049 fp32 on one MI355X.
+
+A step is one forward + backward pass of the reconstruction path over one batch of synthetic
+chains (config 2 draws: lengths ~N(0.145, 0.01) clipped to [0.12, 0.17], angles ~N(2.05,
+0.08), dihedrals ~U(-pi, pi), random anchors, upstream grad ~N(0, 1)), with every input
+already resident in HBM.  The step runs through the public autograd API
+(``reconstruct`` + ``torch.autograd.grad``).
+
+Kernel-level figures come from HIP events recorded on the stream the kernels run on (the
+current torch stream, which the extension launches on) around back-to-back launches of each
+kernel through the C ABI.  ``roofline`` is for the backward kernel (the larger one): its
+algorithmic bytes per launch are 4*B*(9N-12) (read lengths, angles, dihedrals and grad_xyz,
+write the three gradients), against MI355X's 8 TB/s HBM peak.
+
+The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host on a bounded
+sample of chains of the same shape, scaled to atoms/s.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # name: (kind, dtype, B, N)
+    "c1": ("reconstruct", "float32", 1024, 384),
+    "c2": ("reconstruct", "float32", 4096, 2049),
+    "c3": ("torsion", "float32", 8192, 771),
+    "c4_bf16": ("reconstruct", "bfloat16", 16384, 1026),
+    "c4_fp16": ("reconstruct", "float16", 16384, 1026),
+}
+BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
+BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
+DTYPE_CODES = {"float32": 0, "float64": 1, "float16": 2, "bfloat16": 3}
+ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    p.add_argument("--kernel-reps", type=int, default=50)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = auto)")
+    return p.parse_args()
+
+
+def synthetic(B, N, seed, torch, device, dtype):
+    gen = torch.Generator().manual_seed(seed)
+    L = (torch.randn(B, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
+    A = torch.randn(B, N - 2, generator=gen, dtype=torch.float64) * 0.08 + 2.05
+    D = (torch.rand(B, N - 3, generator=gen, dtype=torch.float64) * 2 - 1) * np.pi
+    g = torch.randn(B, N, 3, generator=gen, dtype=torch.float64)
+    p0 = torch.randn(3, generator=gen, dtype=torch.float64)
+    q, _ = torch.linalg.qr(torch.randn(3, 3, generator=gen, dtype=torch.float64))
+    cast = lambda t: t.to(device=device, dtype=dtype).contiguous()  # noqa: E731
+    return cast(L), cast(A), cast(D), cast(g), cast(p0), cast(q[:, 0]), cast(q[:, 1])
+
+
+def event_time_ms(torch, fn, reps):
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(kind, B, N, sample):
+    """Float64 oracle on `sample` chains (fwd + bwd), scaled to atoms/s."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import nerf64 as o
+
+    if kind == "torsion":
+        rng = np.random.default_rng(3)
+        raw = rng.normal(size=(sample, 2 * (N - 3)))
+        g = rng.normal(size=(sample, N, 3))
+        c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+        t0 = time.perf_counter()
+        x = o.torsion_forward(raw, c)
+        o.torsion_backward(raw, x, g, c)
+        dt = time.perf_counter() - t0
+    else:
+        d = o.synthetic_inputs(sample, N, seed=2, anchors=True)
+        an = dict(p0=d["p0"], first_direction=d["first_direction"], initial_normal=d["initial_normal"])
+        t0 = time.perf_counter()
+        o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+        o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **an)
+        dt = time.perf_counter() - t0
+    return sample * N / dt, dt
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (chains shard over the batch "
+            "with no communication, so N GPUs run B/N chains each).",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    import cufk_amd
+
+    kind, dtype_name, B, N = CONFIGS[args.config]
+    dtype = getattr(torch, dtype_name)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    L, A, D, g, p0, fd, n0 = synthetic(B, N, 2, torch, device, dtype)
+    s = ELEM_BYTES[dtype_name]
+
+    if kind == "reconstruct":
+        L.requires_grad_(True)
+        A.requires_grad_(True)
+        D.requires_grad_(True)
+
+        def step():
+            xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
+            return torch.autograd.grad(xyz, (L, A, D), g)
+
+        fwd_bytes = s * B * (6 * N - 6)
+        bwd_bytes = s * B * (9 * N - 12)
+    else:
+        gen = torch.Generator().manual_seed(3)
+        raw = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
+        raw.requires_grad_(True)
+        f = cufk_amd.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+
+        def step():
+            xyz = f(raw)
+            return torch.autograd.grad(xyz, (raw,), g)
+
+        fwd_bytes = s * B * (5 * N - 6)
+        bwd_bytes = s * B * (10 * N - 12)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    # Kernel-level timing through the C ABI (same library the extension links).
+    lib = ctypes.CDLL(str(cufk_amd._native.HIP_LIBRARY))
+    code = DTYPE_CODES[dtype_name]
+    st = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    i64 = ctypes.c_int64
+    if kind == "reconstruct":
+        xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+        gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+
+        def fwd():
+            rc = lib.cufk_reconstruct_fwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), i64(B), i64(N), st)
+            assert rc == 0, rc
+
+        def bwd():
+            rc = lib.cufk_reconstruct_bwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(g), P(gL), P(gA), P(gD),
+                                          i64(B), i64(N), st)
+            assert rc == 0, rc
+    else:
+        import math
+
+        class Consts(ctypes.Structure):
+            _fields_ = [("length", ctypes.c_float * 3), ("sin", ctypes.c_double * 3), ("cos", ctypes.c_double * 3)]
+
+        c = Consts((ctypes.c_float * 3)(*BOND_LENGTHS), (ctypes.c_double * 3)(*[math.sin(a) for a in BOND_ANGLES]),
+                   (ctypes.c_double * 3)(*[math.cos(a) for a in BOND_ANGLES]))
+        xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+        graw = torch.empty_like(raw)
+
+        def fwd():
+            rc = lib.cufk_torsion_fwd(code, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(xyz), i64(B), i64(N), st)
+            assert rc == 0, rc
+
+        def bwd():
+            rc = lib.cufk_torsion_bwd(code, P(raw), i64(raw.stride(0)), P(xyz), P(g), P(graw), i64(graw.stride(0)),
+                                      ctypes.byref(c), i64(B), i64(N), st)
+            assert rc == 0, rc
+
+    t_fwd = event_time_ms(torch, fwd, args.kernel_reps)
+    t_bwd = event_time_ms(torch, bwd, args.kernel_reps)
+
+    atoms = B * N
+    bw_bwd = bwd_bytes / (t_bwd * 1e-3) / 1e9
+    bw_fwd = fwd_bytes / (t_fwd * 1e-3) / 1e9
+    result = {
+        "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
+        "value": atoms / (ms_per_step * 1e-3),
+        "unit": "atoms/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"float32": "f32", "float64": "f64", "float16": "f16", "bfloat16": "bf16"}[dtype_name],
+        "data": "synthetic",
+        "config": {"workload": f"{kind} fwd+bwd", "config": args.config, "batch": B, "points": N,
+                   "dtype": dtype_name, "anchors": "random"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"{kind}_backward",
+            "achieved": bw_bwd,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": bw_bwd / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes": bwd_bytes,
+            "avg_launch_us": t_bwd * 1e3,
+        },
+        "kernels": {
+            "forward_us": t_fwd * 1e3,
+            "backward_us": t_bwd * 1e3,
+            "forward_GBs": bw_fwd,
+            "fwd_plus_bwd_us": (t_fwd + t_bwd) * 1e3,
+            "fwd_plus_bwd_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / ((t_fwd + t_bwd) * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "fwd_plus_bwd_atoms_per_s": atoms / ((t_fwd + t_bwd) * 1e-3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        sample = args.cpu_sample or (64 if kind == "reconstruct" else 128)
+        v, dt = cpu_baseline(kind, B, N, sample)
+        result["cpu_baseline"] = {
+            "value": v,
+            "unit": "atoms/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"float64 numpy oracle, fwd+bwd of {sample} chains x N={N} ({dt:.1f} s), scaled to atoms/s",
+        }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

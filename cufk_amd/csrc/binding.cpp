@@ -1,0 +1,299 @@
+// PyTorch-ROCm extension cufk_amd._C: autograd wrappers and input validation over the C ABI
+// of libcufk_hip.so.  Mirrors the reference's C++ layer (paths under src/cufk/csrc/):
+//   ReconstructAutograd + apply      block.cu:367-445
+//   TorsionAutograd + apply          torsion.cu:413-447
+//   validation messages              extension_utils.cuh:57-130
+// All device work goes through cufk_* entry points on the current HIP stream of the
+// input's device; nothing here launches kernels itself.
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <array>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "cufk_hip.h"
+
+namespace {
+
+using torch::Tensor;
+using TensorList = std::vector<Tensor>;
+
+bool supported_dtype(torch::ScalarType t) {
+  return t == torch::kFloat32 || t == torch::kFloat64 || t == torch::kFloat16 || t == torch::kBFloat16;
+}
+
+// extension_utils.cuh:35-51 dispatch_dtype.
+int dtype_code(const Tensor& x) {
+  switch (x.scalar_type()) {
+    case torch::kFloat32: return CUFK_FLOAT32;
+    case torch::kFloat64: return CUFK_FLOAT64;
+    case torch::kFloat16: return CUFK_FLOAT16;
+    case torch::kBFloat16: return CUFK_BFLOAT16;
+    default: break;
+  }
+  TORCH_CHECK(false, "unsupported dtype");
+  return -1;
+}
+
+// extension_utils.cuh:57-61.  `device` false skips the device-type check so that the rest of
+// the contract can be exercised with host tensors.
+void check_cuda_float(const Tensor& x, const char* name, bool device) {
+  TORCH_CHECK(!device || x.is_cuda(), name, " must be CUDA");
+  TORCH_CHECK(supported_dtype(x.scalar_type()), name, " must be float32, float64, float16, or bfloat16");
+  TORCH_CHECK(x.is_contiguous(), name, " must be contiguous");
+}
+
+// extension_utils.cuh:63-68.
+void check_cuda_float_row_contiguous(const Tensor& x, const char* name, bool device) {
+  TORCH_CHECK(!device || x.is_cuda(), name, " must be CUDA");
+  TORCH_CHECK(supported_dtype(x.scalar_type()), name, " must be float32, float64, float16, or bfloat16");
+  TORCH_CHECK(x.dim() == 2, name, " must have shape (B, K)");
+  TORCH_CHECK(x.stride(1) == 1, name, " must have stride(1) == 1");
+}
+
+// extension_utils.cuh:70-74.
+void check_like(const Tensor& x, const Tensor& ref, const char* name, bool device) {
+  check_cuda_float(x, name, device);
+  TORCH_CHECK(x.scalar_type() == ref.scalar_type(), name, " must have the same dtype as reference");
+  TORCH_CHECK(x.device() == ref.device(), name, " must be on the same device as reference");
+}
+
+// extension_utils.cuh:76-82.
+void check_anchor(const Tensor& x, const Tensor& ref, const char* name, bool device) {
+  TORCH_CHECK(!device || x.is_cuda(), name, " must be CUDA");
+  TORCH_CHECK(x.scalar_type() == ref.scalar_type(), name, " must have the same dtype as reference");
+  TORCH_CHECK(x.device() == ref.device(), name, " must be on the same device as reference");
+  TORCH_CHECK(x.sizes() == torch::IntArrayRef({3}), name, " must have shape (3,)");
+  TORCH_CHECK(!x.requires_grad(), name, " gradients are not supported");
+}
+
+struct Shape {
+  int64_t batch;
+  int64_t points;
+};
+
+// extension_utils.cuh:119-126.
+Shape chain_shape_from_steps(const Tensor& ref, int64_t steps) {
+  TORCH_CHECK(ref.size(0) <= INT32_MAX && steps + 3 <= INT32_MAX, "shape exceeds int32 kernel limits");
+  TORCH_CHECK(steps >= 1, "point_count must be >= 4");
+  return {ref.size(0), steps + 3};
+}
+
+// extension_utils.cuh:128-130.
+void check_max_local_transforms(int64_t steps, int64_t max_steps, const char* op_name) {
+  TORCH_CHECK(steps <= max_steps, op_name, " supports at most ", max_steps, " local transforms");
+}
+
+// block.cu:367-378.
+Shape check_geom(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, bool device) {
+  check_cuda_float(lengths, "lengths", device);
+  check_like(angles, lengths, "angles", device);
+  check_like(dihedrals, lengths, "dihedrals", device);
+  TORCH_CHECK(lengths.dim() == 2, "lengths must have shape (B, N-1)");
+  TORCH_CHECK(angles.dim() == 2, "angles must have shape (B, N-2)");
+  TORCH_CHECK(dihedrals.dim() == 2, "dihedrals must have shape (B, N-3)");
+  const Shape shape = chain_shape_from_steps(lengths, lengths.size(1) - 2);
+  TORCH_CHECK(angles.sizes() == torch::IntArrayRef({shape.batch, shape.points - 2}), "bad angles shape");
+  TORCH_CHECK(dihedrals.sizes() == torch::IntArrayRef({shape.batch, shape.points - 3}), "bad dihedrals shape");
+  return shape;
+}
+
+struct Anchors {
+  Tensor p0, first_direction, initial_normal;
+};
+
+// extension_utils.cuh:90-103.
+Anchors checked_anchors(const Tensor& p0, const Tensor& fd, const Tensor& n0, const Tensor& ref, bool device) {
+  check_anchor(p0, ref, "p0", device);
+  check_anchor(fd, ref, "first_direction", device);
+  check_anchor(n0, ref, "initial_normal", device);
+  return {p0.contiguous(), fd.contiguous(), n0.contiguous()};
+}
+
+// torsion.cu:413-417.
+Shape check_pairs(const Tensor& raw_pairs, bool device) {
+  check_cuda_float_row_contiguous(raw_pairs, "raw_pairs", device);
+  TORCH_CHECK(raw_pairs.size(1) % 2 == 0, "raw_pairs second dimension must be even");
+  return chain_shape_from_steps(raw_pairs, raw_pairs.size(1) / 2);
+}
+
+int max_steps(const Tensor& ref, int direction) {
+  const int m = cufk_max_steps(dtype_code(ref), direction, ref.get_device());
+  TORCH_CHECK(m >= 0, "cufk_max_steps: ", cufk_error_string(-m));
+  return m;
+}
+
+void* current_stream(const Tensor& ref) { return c10::hip::getCurrentHIPStream(ref.get_device()).stream(); }
+
+void check_status(int status, const char* what) {
+  TORCH_CHECK(status == CUFK_OK, what, " failed: ", cufk_error_string(status));
+}
+
+// ------------------------------------------------------------------ reconstruct
+
+class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
+                        Tensor p0, Tensor first_direction, Tensor initial_normal) {
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    const c10::DeviceGuard guard(lengths.device());
+    check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    check_status(cufk_reconstruct_fwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
+                                      a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
+                                      xyz.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_fwd");
+    ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
+    return xyz;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& lengths = saved[0];
+    const Tensor& angles = saved[1];
+    const Tensor& dihedrals = saved[2];
+    Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_points, lengths, "grad_points", true);
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true);
+    const c10::DeviceGuard guard(lengths.device());
+    const int64_t steps = shape.points - 3;
+    const int64_t limit = max_steps(lengths, CUFK_BACKWARD);
+    // block.cu:335-345 (this build has no shared-memory cap below the plan cap).
+    TORCH_CHECK(steps <= limit, "backward supports at most ", limit, " local transforms for this dtype/device, got ", steps,
+                " (plan cap ", limit, ", shared-memory cap ", limit, ")");
+    Tensor grad_lengths = torch::empty_like(lengths);
+    Tensor grad_angles = torch::empty_like(angles);
+    Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    check_status(cufk_reconstruct_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
+                                      a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
+                                      grad_points.data_ptr(), grad_lengths.data_ptr(), grad_angles.data_ptr(),
+                                      grad_dihedrals.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_bwd");
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor()};
+  }
+};
+
+Tensor apply_reconstruct(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
+                         const Tensor& first_direction, const Tensor& initial_normal) {
+  return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
+}
+
+// ------------------------------------------------------------------ torsion
+
+cufk_torsion_consts consts_from(const std::vector<double>& packed) {
+  cufk_torsion_consts c;
+  for (int i = 0; i < 3; ++i) {
+    c.length[i] = static_cast<float>(packed[i]);
+    c.sin[i] = packed[3 + i];
+    c.cos[i] = packed[6 + i];
+  }
+  return c;
+}
+
+class TorsionAutograd : public torch::autograd::Function<TorsionAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor raw_pairs, std::vector<double> packed) {
+    const Shape shape = check_pairs(raw_pairs, true);
+    const c10::DeviceGuard guard(raw_pairs.device());
+    check_max_local_transforms(shape.points - 3, max_steps(raw_pairs, CUFK_FORWARD), "torsion_pairs");
+    const cufk_torsion_consts c = consts_from(packed);
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, raw_pairs.options());
+    check_status(cufk_torsion_fwd(dtype_code(raw_pairs), raw_pairs.data_ptr(), raw_pairs.stride(0), &c, xyz.data_ptr(),
+                                  shape.batch, shape.points, current_stream(raw_pairs)),
+                 "cufk_torsion_fwd");
+    ctx->save_for_backward({raw_pairs, xyz});
+    ctx->saved_data["consts"] = c10::List<double>(packed);
+    return xyz;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& raw_pairs = saved[0];
+    const Tensor& xyz = saved[1];
+    Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_points, raw_pairs, "grad_points", true);
+    const Shape shape = check_pairs(raw_pairs, true);
+    const c10::DeviceGuard guard(raw_pairs.device());
+    check_max_local_transforms(shape.points - 3, max_steps(raw_pairs, CUFK_FORWARD), "torsion_pairs");
+    const auto list = ctx->saved_data["consts"].toDoubleList();
+    const cufk_torsion_consts c = consts_from(std::vector<double>(list.begin(), list.end()));
+    // extension_utils.cuh:162-164: the gradient keeps the raw tensor's strides.
+    Tensor grad = torch::empty_strided(raw_pairs.sizes(), raw_pairs.strides(), raw_pairs.options());
+    check_status(cufk_torsion_bwd(dtype_code(raw_pairs), raw_pairs.data_ptr(), raw_pairs.stride(0), xyz.data_ptr(),
+                                  grad_points.data_ptr(), grad.data_ptr(), grad.stride(0), &c, shape.batch, shape.points,
+                                  current_stream(raw_pairs)),
+                 "cufk_torsion_bwd");
+    return {grad, Tensor()};
+  }
+};
+
+// A compiled torsion reconstructor: the three bond lengths and bond-angle sin/cos fixed at
+// construction (torsion.py:89-135 compiles them into a JIT module instead).
+class TorsionModule {
+ public:
+  TorsionModule(const std::vector<double>& lengths, const std::vector<double>& sins, const std::vector<double>& coss) {
+    TORCH_CHECK(lengths.size() == 3 && sins.size() == 3 && coss.size() == 3, "torsion constants must have 3 elements");
+    packed_.reserve(9);
+    for (double v : lengths) packed_.push_back(static_cast<double>(static_cast<float>(v)));
+    for (double v : sins) packed_.push_back(v);
+    for (double v : coss) packed_.push_back(v);
+  }
+  Tensor apply(const Tensor& raw_pairs) const { return TorsionAutograd::apply(raw_pairs, packed_); }
+  std::vector<double> lengths() const { return {packed_[0], packed_[1], packed_[2]}; }
+  std::vector<double> sins() const { return {packed_[3], packed_[4], packed_[5]}; }
+  std::vector<double> coss() const { return {packed_[6], packed_[7], packed_[8]}; }
+
+ private:
+  std::vector<double> packed_;
+};
+
+// ------------------------------------------------------------------ host-side contract hooks
+
+std::vector<int64_t> validate_reconstruct(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals,
+                                          const Tensor& p0, const Tensor& first_direction, const Tensor& initial_normal,
+                                          bool device) {
+  const Shape shape = check_geom(lengths, angles, dihedrals, device);
+  checked_anchors(p0, first_direction, initial_normal, lengths, device);
+  check_max_local_transforms(shape.points - 3, cufk_max_steps(dtype_code(lengths), CUFK_FORWARD, 0), "reconstruct");
+  return {shape.batch, shape.points};
+}
+
+void validate_grad_points(const Tensor& grad_points, const Tensor& lengths, bool device) {
+  check_like(grad_points, lengths, "grad_points", device);
+}
+
+std::vector<int64_t> validate_torsion(const Tensor& raw_pairs, bool device) {
+  const Shape shape = check_pairs(raw_pairs, device);
+  check_max_local_transforms(shape.points - 3, cufk_max_steps(dtype_code(raw_pairs), CUFK_FORWARD, 0), "torsion_pairs");
+  return {shape.batch, shape.points};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("apply", &apply_reconstruct, "reconstruct autograd apply (block.cu:443-445)", py::arg("lengths"),
+        py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
+  py::class_<TorsionModule>(m, "TorsionModule")
+      .def(py::init<const std::vector<double>&, const std::vector<double>&, const std::vector<double>&>(),
+           py::arg("lengths"), py::arg("sin"), py::arg("cos"))
+      .def("apply", &TorsionModule::apply, "torsion-only autograd apply (torsion.cu:445-447)", py::arg("raw_pairs"))
+      .def("__call__", &TorsionModule::apply, py::arg("raw_pairs"))
+      .def_property_readonly("lengths", &TorsionModule::lengths)
+      .def_property_readonly("sin", &TorsionModule::sins)
+      .def_property_readonly("cos", &TorsionModule::coss);
+  m.def("validate_reconstruct", &validate_reconstruct, py::arg("lengths"), py::arg("angles"), py::arg("dihedrals"),
+        py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"), py::arg("device") = true);
+  m.def("validate_grad_points", &validate_grad_points, py::arg("grad_points"), py::arg("lengths"),
+        py::arg("device") = true);
+  m.def("validate_torsion", &validate_torsion, py::arg("raw_pairs"), py::arg("device") = true);
+  m.def("max_steps", [](int dtype, int direction, int device) { return cufk_max_steps(dtype, direction, device); });
+  m.def("library_version", []() { return std::string(cufk_version()); });
+}

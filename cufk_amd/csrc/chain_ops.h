@@ -1,0 +1,318 @@
+// Device primitives for the NeRF chain scan on CDNA4 (gfx950, wave64).
+//
+// A chain step k maps internal coordinates (l, theta, phi) = (L[k+2], A[k+1], D[k]) to the
+// rigid transform M = Rx(phi) * Rz(pi - theta) with translation l * M[:,0]
+// (reference: src/cufk/csrc/affine.cuh:24-51).  The running product of these transforms
+// is a rotation R (row-major R[r][c]) plus a translation; the reference composes general
+// 3x4 affines (affine.cuh:53-58), here a new step is folded into a running rotation with
+// two column rotations (24 FMA) and its translation is l times the new first column (3 FMA).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+
+namespace cufk_amd {
+
+// ------------------------------------------------------------------ scalar types
+
+// Storage types: float, double, _Float16 (torch.float16), __bf16 (torch.bfloat16).
+// Compute type: double for double, float otherwise.  Half types are widened on load and
+// rounded once on store (the reference instead rounds every payload operation to the
+// storage type, scalar.cuh:8-92; see the design notes for why this build does not).
+template <typename T> struct compute_type { using type = float; };
+template <> struct compute_type<double> { using type = double; };
+template <typename T> using compute_t = typename compute_type<T>::type;
+
+template <typename T> __device__ __forceinline__ compute_t<T> widen(T x) {
+  return static_cast<compute_t<T>>(x);
+}
+template <typename T> __device__ __forceinline__ T narrow(compute_t<T> x) {
+  return static_cast<T>(x);
+}
+
+// sin and cos of a float argument evaluated in double: Cody-Waite reduction by pi/2 (two-part
+// constant) and Taylor polynomials through r^11 / r^12 (truncation < 1e-11 on |r| <= pi/4).
+// Rounded to float the results agree with correct rounding except in a few inputs per
+// million, so s^2 + c^2 - 1 has no systematic bias.  (The library sincosf carries a bias of
+// about -1.5e-8 in s^2 + c^2 that compounds into a scale drift along a 2000-step chain.)
+// FP64 FMA issues at the non-packed FP32 rate on CDNA3/4, so this costs about as much as the
+// float library routine.  |x| > 65536 and non-finite x take the library path.
+__device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
+  if (!(fabsf(xf) <= 65536.0f)) {
+    sincos(static_cast<double>(xf), &s, &c);
+    return;
+  }
+  const double x = xf;
+  const double k = __builtin_rint(x * 0.63661977236758134308);
+  double r = fma(-k, 1.5707963267948966, x);
+  r = fma(-k, 6.123233995736766e-17, r);
+  const double r2 = r * r;
+  double ps = -2.505210838544172e-08;
+  ps = fma(ps, r2, 2.7557319223985893e-06);
+  ps = fma(ps, r2, -0.0001984126984126984);
+  ps = fma(ps, r2, 0.008333333333333333);
+  ps = fma(ps, r2, -0.16666666666666666);
+  const double sn = fma(r * r2, ps, r);
+  double pc = 2.08767569878681e-09;
+  pc = fma(pc, r2, -2.755731922398589e-07);
+  pc = fma(pc, r2, 2.48015873015873e-05);
+  pc = fma(pc, r2, -0.001388888888888889);
+  pc = fma(pc, r2, 0.041666666666666664);
+  pc = fma(pc, r2, -0.5);
+  const double cs = fma(r2, pc, 1.0);
+  const int q = static_cast<int>(k) & 3;
+  const double so = (q & 1) ? cs : sn;
+  const double co = (q & 1) ? sn : cs;
+  s = (q & 2) ? -so : so;
+  c = ((q + 1) & 2) ? -co : co;
+}
+__device__ __forceinline__ void sin_cos_wide(double x, double& s, double& c) { sincos(x, &s, &c); }
+
+// Unit (sin, cos) from a raw pair in double (torsion.cu:119-141 clamps rs^2 + rc^2 at 1e-16).
+template <typename R> __device__ __forceinline__ void pair_unit(R rs, R rc, double& S, double& C) {
+  const double a = rs, b = rc;
+  const double n2 = a * a + b * b;
+  const double eps2 = static_cast<double>(1.0e-8f * 1.0e-8f);
+  const double rinv = 1.0 / sqrt(n2 < eps2 ? eps2 : n2);
+  S = a * rinv;
+  C = b * rinv;
+}
+
+__device__ __forceinline__ float sqrt_r(float x) { return sqrtf(x); }
+__device__ __forceinline__ double sqrt_r(double x) { return sqrt(x); }
+
+// ------------------------------------------------------------------ small vectors
+
+template <typename R> struct V3 {
+  R x, y, z;
+};
+
+template <typename R> __device__ __forceinline__ V3<R> operator+(V3<R> a, V3<R> b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
+template <typename R> __device__ __forceinline__ V3<R> operator-(V3<R> a, V3<R> b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
+template <typename R> __device__ __forceinline__ V3<R> operator*(R s, V3<R> a) { return {s * a.x, s * a.y, s * a.z}; }
+template <typename R> __device__ __forceinline__ R dot(V3<R> a, V3<R> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+template <typename R> __device__ __forceinline__ V3<R> cross(V3<R> a, V3<R> b) {
+  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+
+// frame_utils.cuh:17-21: v / sqrt(max(v.v, eps)) with eps = 1e-12f.
+template <typename R> __device__ __forceinline__ V3<R> normalized(V3<R> v) {
+  const R n2 = dot(v, v);
+  const R eps = static_cast<R>(1.0e-12f);
+  const R n = sqrt_r(n2 > eps ? n2 : eps);
+  return {v.x / n, v.y / n, v.z / n};
+}
+
+// ------------------------------------------------------------------ rigid transforms
+
+// Rotation (row-major) plus translation.  12 scalars.
+template <typename R> struct Rigid {
+  R m[9];
+  R v[3];
+};
+
+template <typename R> __device__ __forceinline__ Rigid<R> rigid_identity() {
+  Rigid<R> a;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) a.m[i] = (i % 4 == 0) ? R(1) : R(0);
+  a.v[0] = a.v[1] = a.v[2] = R(0);
+  return a;
+}
+
+// (a o b): rotation a.m b.m, translation a.v + a.m b.v; a is the earlier transform
+// (reference affine.cuh:53-58, scan.cuh:48).
+template <typename R> __device__ __forceinline__ Rigid<R> compose(const Rigid<R>& a, const Rigid<R>& b) {
+  Rigid<R> o;
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      o.m[3 * r + c] = a.m[3 * r] * b.m[c] + a.m[3 * r + 1] * b.m[3 + c] + a.m[3 * r + 2] * b.m[6 + c];
+    o.v[r] = a.v[r] + a.m[3 * r] * b.v[0] + a.m[3 * r + 1] * b.v[1] + a.m[3 * r + 2] * b.v[2];
+  }
+  return o;
+}
+
+template <typename R, typename S> __device__ __forceinline__ Rigid<R> narrow_rigid(const Rigid<S>& a) {
+  Rigid<R> o;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) o.m[i] = static_cast<R>(a.m[i]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) o.v[i] = static_cast<R>(a.v[i]);
+  return o;
+}
+
+template <typename R> __device__ __forceinline__ V3<R> rot_apply(const R (&m)[9], V3<R> x) {
+  return {m[0] * x.x + m[1] * x.y + m[2] * x.z, m[3] * x.x + m[4] * x.y + m[5] * x.z, m[6] * x.x + m[7] * x.y + m[8] * x.z};
+}
+
+// R <- R * Rx(phi) * Rz(pi - theta), translation += l * (new R)[:,0].
+// Equals composing with the reference local transform (affine.cuh:36-45).
+template <typename R>
+__device__ __forceinline__ void step_forward(R (&m)[9], R (&v)[3], R l, R s, R c, R S, R C) {
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const R q0 = m[3 * r], q1 = m[3 * r + 1], q2 = m[3 * r + 2];
+    const R a1 = C * q1 + S * q2;
+    const R a2 = C * q2 - S * q1;
+    const R n0 = s * a1 - c * q0;
+    const R n1 = -(s * q0) - c * a1;
+    m[3 * r] = n0;
+    m[3 * r + 1] = n1;
+    m[3 * r + 2] = a2;
+    v[r] = v[r] + l * n0;
+  }
+}
+
+// Inverse of the rotation part of step_forward: R <- R * Rz(pi - theta)^T * Rx(phi)^T.
+template <typename R>
+__device__ __forceinline__ void step_backward(R (&m)[9], R s, R c, R S, R C) {
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const R n0 = m[3 * r], n1 = m[3 * r + 1], a2 = m[3 * r + 2];
+    const R q0 = -(c * n0) - s * n1;
+    const R a1 = s * n0 - c * n1;
+    m[3 * r] = q0;
+    m[3 * r + 1] = C * a1 - S * a2;
+    m[3 * r + 2] = S * a1 + C * a2;
+  }
+}
+
+// ------------------------------------------------------------------ first frame
+
+// block.cu:113-148 compute_first_frame (A.2): p1, p2, d0, t0, d1, frame = [d1 | n x d1 | n].
+template <typename R> struct FirstFrame {
+  V3<R> p0, p1, p2, d0, t0, d1;
+  R frame[9];  // row-major
+};
+
+template <typename T>
+__device__ __forceinline__ FirstFrame<compute_t<T>> first_frame(compute_t<T> L0, compute_t<T> L1, compute_t<T> A0,
+                                                                const T* __restrict__ p0, const T* __restrict__ fd,
+                                                                const T* __restrict__ n0) {
+  using R = compute_t<T>;
+  FirstFrame<R> f;
+  f.p0 = {widen(p0[0]), widen(p0[1]), widen(p0[2])};
+  f.d0 = normalized(V3<R>{widen(fd[0]), widen(fd[1]), widen(fd[2])});
+  f.p1 = f.p0 + L0 * f.d0;
+  V3<R> nn = {widen(n0[0]), widen(n0[1]), widen(n0[2])};
+  nn = nn - dot(nn, f.d0) * f.d0;
+  if (dot(nn, nn) < static_cast<R>(1.0e-12f)) {  // block.cu:41,126; frame_utils.cuh:23-31
+    const bool use_y = fabs(f.d0.x) >= R(0.9);
+    const V3<R> helper = {use_y ? R(0) : R(1), use_y ? R(1) : R(0), R(0)};
+    nn = normalized(cross(f.d0, helper));
+  } else {
+    nn = normalized(nn);
+  }
+  f.t0 = normalized(cross(nn, f.d0));
+  double sd, cd;
+  sin_cos_wide(A0, sd, cd);
+  const R s = static_cast<R>(sd), c = static_cast<R>(cd);
+  f.d1 = (-c) * f.d0 + s * f.t0;
+  f.p2 = f.p1 + L1 * f.d1;
+  const V3<R> n = normalized(cross(f.d0, f.d1));
+  const V3<R> side = cross(n, f.d1);
+  f.frame[0] = f.d1.x; f.frame[1] = side.x; f.frame[2] = n.x;
+  f.frame[3] = f.d1.y; f.frame[4] = side.y; f.frame[5] = n.y;
+  f.frame[6] = f.d1.z; f.frame[7] = side.z; f.frame[8] = n.z;
+  return f;
+}
+
+// ------------------------------------------------------------------ wave64 scans
+
+// DPP controls (GFX9 encoding, valid on gfx950).
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
+// Lane value moved by DPP; lanes whose source is outside the pattern (or whose row is
+// masked off) receive `old`.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ float dpp_move(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
+                                                               Ctrl, RowMask, 0xf, false));
+}
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ double dpp_move(double old, double src) {
+  const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, src);
+  const int lo = __builtin_amdgcn_update_dpp(static_cast<int>(o), static_cast<int>(x), Ctrl, RowMask, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(static_cast<int>(o >> 32), static_cast<int>(x >> 32), Ctrl, RowMask, 0xf, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
+template <int Ctrl, int RowMask, typename R>
+__device__ __forceinline__ Rigid<R> dpp_rigid(const Rigid<R>& x) {
+  Rigid<R> y;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) y.m[i] = dpp_move<Ctrl, RowMask>((i % 4 == 0) ? R(1) : R(0), x.m[i]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) y.v[i] = dpp_move<Ctrl, RowMask>(R(0), x.v[i]);
+  return y;
+}
+
+// Inclusive left-to-right scan of rigid transforms over the 64 lanes of a wave:
+// four row_shr rounds inside each 16-lane row, then row_bcast:15 and row_bcast:31.
+template <typename R> __device__ __forceinline__ Rigid<R> wave_prefix(Rigid<R> x) {
+  x = compose(dpp_rigid<kRowShr1, 0xf>(x), x);
+  x = compose(dpp_rigid<kRowShr2, 0xf>(x), x);
+  x = compose(dpp_rigid<kRowShr4, 0xf>(x), x);
+  x = compose(dpp_rigid<kRowShr8, 0xf>(x), x);
+  x = compose(dpp_rigid<kRowBcast15, 0xa>(x), x);
+  x = compose(dpp_rigid<kRowBcast31, 0xc>(x), x);
+  return x;
+}
+
+// Value of lane-1 (identity in lane 0).
+template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up(const Rigid<R>& x, int lane) {
+  Rigid<R> y;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    const R t = __shfl_up(x.m[i], 1);
+    y.m[i] = lane == 0 ? ((i % 4 == 0) ? R(1) : R(0)) : t;
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const R t = __shfl_up(x.v[i], 1);
+    y.v[i] = lane == 0 ? R(0) : t;
+  }
+  return y;
+}
+
+// Additive force/moment pair (torsion.cu:184-211).
+template <typename R> struct ForceMoment {
+  V3<R> f, m;
+};
+
+template <typename R> __device__ __forceinline__ R shfl_down_or_zero(R x, int d, int lane) {
+  const R t = __shfl_down(x, d);
+  return lane + d < 64 ? t : R(0);
+}
+
+// Inclusive right-to-left (suffix) sum over the lanes of a wave.
+template <typename R> __device__ __forceinline__ ForceMoment<R> wave_suffix(ForceMoment<R> a, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    a.f.x += shfl_down_or_zero(a.f.x, d, lane);
+    a.f.y += shfl_down_or_zero(a.f.y, d, lane);
+    a.f.z += shfl_down_or_zero(a.f.z, d, lane);
+    a.m.x += shfl_down_or_zero(a.m.x, d, lane);
+    a.m.y += shfl_down_or_zero(a.m.y, d, lane);
+    a.m.z += shfl_down_or_zero(a.m.z, d, lane);
+  }
+  return a;
+}
+
+template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(const ForceMoment<R>& a, int lane) {
+  ForceMoment<R> b;
+  b.f.x = shfl_down_or_zero(a.f.x, 1, lane);
+  b.f.y = shfl_down_or_zero(a.f.y, 1, lane);
+  b.f.z = shfl_down_or_zero(a.f.z, 1, lane);
+  b.m.x = shfl_down_or_zero(a.m.x, 1, lane);
+  b.m.y = shfl_down_or_zero(a.m.y, 1, lane);
+  b.m.z = shfl_down_or_zero(a.m.z, 1, lane);
+  return b;
+}
+
+}  // namespace cufk_amd

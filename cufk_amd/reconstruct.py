@@ -1,0 +1,75 @@
+"""Generic reconstruction path: ``reconstruct(lengths, angles, dihedrals, p0, first_direction, initial_normal)``.
+
+Mirrors the reference ``src/cufk/reconstruct.py:1-81``: same batching of 1-D inputs, same
+default anchors, same contiguity handling, same call into ``_C.apply`` (a C++
+``torch::autograd::Function`` over the HIP C ABI).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._native import _C
+
+# reconstruct.py:5: N <= 2051 points (2048 local transforms).
+BLOCK_SCAN_MAX_POINT_COUNT = 2051
+
+
+def _batched_inputs(
+    lengths: torch.Tensor,
+    angles: torch.Tensor,
+    dihedrals: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, bool]:
+    """reconstruct.py:8-16: add a batch axis when ``lengths`` is 1-D."""
+    single = lengths.dim() == 1
+    if single:
+        lengths, angles, dihedrals = lengths[None], angles[None], dihedrals[None]
+    return lengths, angles, dihedrals, single
+
+
+def _anchor(x: torch.Tensor | None, vals: tuple[float, float, float], ref: torch.Tensor) -> torch.Tensor:
+    """reconstruct.py:19-26: default anchor on ``ref``'s device and dtype."""
+    if x is None:
+        x = torch.tensor(vals, device=ref.device, dtype=ref.dtype)
+    return x
+
+
+def reconstruct(
+    lengths: torch.Tensor,
+    angles: torch.Tensor,
+    dihedrals: torch.Tensor,
+    p0: torch.Tensor | None = None,
+    first_direction: torch.Tensor | None = None,
+    initial_normal: torch.Tensor | None = None,
+) -> torch.Tensor:
+    r"""Reconstruct Cartesian coordinates from full internal coordinates.
+
+    Args:
+        lengths: Bond lengths, GPU tensor ``(N - 1,)`` for one chain or ``(B, N - 1)``.
+        angles: Bond angles in radians, ``(N - 2,)`` or ``(B, N - 2)``.
+        dihedrals: Dihedral angles in radians, ``(N - 3,)`` or ``(B, N - 3)``.
+        p0: Optional first point ``(3,)``; defaults to ``(0, 0, 0)``.
+        first_direction: Optional first-bond direction ``(3,)``; defaults to ``(1, 0, 0)``.
+        initial_normal: Optional initial plane normal ``(3,)``; defaults to ``(0, 0, 1)``.
+
+    Returns:
+        ``(N, 3)`` for one chain or ``(B, N, 3)``, dtype of ``lengths``.
+
+    All inputs are GPU tensors of one dtype (float16, bfloat16, float32 or float64),
+    4 <= N <= 2051.  Gradients flow to lengths, angles and dihedrals; anchors must not
+    require grad.
+    """
+    lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
+    p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
+    first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
+    initial_normal = _anchor(initial_normal, (0.0, 0.0, 1.0), lengths)
+
+    xyz = _C.apply(
+        lengths.contiguous(),
+        angles.contiguous(),
+        dihedrals.contiguous(),
+        p0,
+        first_direction,
+        initial_normal,
+    )
+    return xyz[0] if single else xyz

@@ -1,0 +1,113 @@
+/*
+ * cufk_hip.h -- C ABI of the MI355X (gfx950) NeRF chain-reconstruction library.
+ *
+ * Plain device pointers and sizes; no torch types.  Every entry point enqueues work on
+ * `stream` (a hipStream_t passed as void*; NULL = the default stream) and returns a status
+ * code without synchronising.  Tensors are dense row-major: chain b of an (B, K) array
+ * starts at element b*K, except torsion raw pairs whose row stride is explicit.
+ *
+ * Reference entry points replaced (paths under the reference tree src/cufk/):
+ *   cufk._C.apply forward        csrc/block.cu:319-329 (forward_cuda_impl), 393-410
+ *   cufk._C.apply backward       csrc/block.cu:331-365 (backward_cuda_impl), 412-428
+ *   torsion module apply fwd     csrc/torsion.cu:387-397 (forward_default_impl), 421-426
+ *   torsion module apply bwd     csrc/torsion.cu:399-411 (backward_xyz_impl), 428-436
+ *   step caps                    csrc/block.cu:88, 334-345; csrc/extension_utils.cuh:128-130,190-199
+ */
+#ifndef CUFK_HIP_H
+#define CUFK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (csrc/extension_utils.cuh:35-51 dispatch_dtype). */
+enum cufk_dtype {
+  CUFK_FLOAT32 = 0,
+  CUFK_FLOAT64 = 1,
+  CUFK_FLOAT16 = 2,
+  CUFK_BFLOAT16 = 3
+};
+
+/* Status codes. */
+enum cufk_status {
+  CUFK_OK = 0,
+  CUFK_ERR_DTYPE = 1,       /* "unsupported dtype" (extension_utils.cuh:49) */
+  CUFK_ERR_POINTS = 2,      /* "point_count must be >= 4" (extension_utils.cuh:121) */
+  CUFK_ERR_SHAPE = 3,       /* "shape exceeds int32 kernel limits" (extension_utils.cuh:120) */
+  CUFK_ERR_STEPS = 4,       /* more local transforms than the step cap (extension_utils.cuh:128-130) */
+  CUFK_ERR_NULL = 5,        /* a required pointer is NULL while B > 0 */
+  CUFK_ERR_STRIDE = 6,      /* raw-pair row stride shorter than the row */
+  CUFK_ERR_LAUNCH = 7,      /* kernel launch failed (C10_CUDA_KERNEL_LAUNCH_CHECK, block.cu:327) */
+  CUFK_ERR_DEVICE = 8       /* device query failed */
+};
+
+/* Direction argument of cufk_max_steps. */
+enum cufk_direction { CUFK_FORWARD = 0, CUFK_BACKWARD = 1 };
+
+/*
+ * Compiled torsion constants (csrc/torsion.cu:43-53; torsion.py:81-86): bond lengths are
+ * float even for float64 chains, bond-angle sin/cos are float64 values.  Step k uses
+ * length[(k+2)%3] and angle (k+1)%3 (torsion.cu:67-73).
+ */
+typedef struct cufk_torsion_consts {
+  float length[3];
+  double sin[3];
+  double cos[3];
+} cufk_torsion_consts;
+
+/*
+ * Forward reconstruction.  Replaces block.cu:319-329 (forward_cuda_impl) and its launch of
+ * block_forward_kernel (block.cu:157-204).
+ *   lengths (B, N-1), angles (B, N-2), dihedrals (B, N-3); anchors p0, first_direction,
+ *   initial_normal (3,) each; xyz (B, N, 3) output.  4 <= N <= 2051.
+ */
+int cufk_reconstruct_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                         const void* p0, const void* first_direction, const void* initial_normal,
+                         void* xyz, int64_t batch, int64_t points, void* stream);
+
+/*
+ * Backward reconstruction: dL/d(lengths, angles, dihedrals) from grad_xyz (B, N, 3).
+ * Replaces block.cu:331-365 (backward_cuda_impl) and block_backward_kernel
+ * (block.cu:230-313).  The anchors receive no gradient (block.cu:427).
+ */
+int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                         const void* p0, const void* first_direction, const void* initial_normal,
+                         const void* grad_xyz, void* grad_lengths, void* grad_angles, void* grad_dihedrals,
+                         int64_t batch, int64_t points, void* stream);
+
+/*
+ * Torsion-only forward from raw interleaved (sin, cos) pairs, raw row b at
+ * raw + b*raw_stride (elements), 2*(N-3) values per row.  xyz (B, N, 3) dense.
+ * Replaces torsion.cu:387-397 and forward_kernel (torsion.cu:254-295).
+ */
+int cufk_torsion_fwd(int dtype, const void* raw_pairs, int64_t raw_stride, const cufk_torsion_consts* consts,
+                     void* xyz, int64_t batch, int64_t points, void* stream);
+
+/*
+ * Torsion-only backward: grad_raw (row stride grad_raw_stride) from the saved forward xyz
+ * and grad_xyz.  Replaces torsion.cu:399-411 and backward_kernel (torsion.cu:297-381).
+ */
+int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const void* xyz, const void* grad_xyz,
+                     void* grad_raw, int64_t grad_raw_stride, const cufk_torsion_consts* consts, int64_t batch,
+                     int64_t points, void* stream);
+
+/*
+ * Largest step count (N-3) accepted for (dtype, direction) on `device`, or a negative
+ * status.  Replaces kMaxSteps (block.cu:88, torsion.cu:97) and dynamic_shared_plan_limit
+ * (extension_utils.cuh:190-199).
+ */
+int cufk_max_steps(int dtype, int direction, int device);
+
+/* Static text for a status code. */
+const char* cufk_error_string(int status);
+
+/* Library version, "major.minor.patch". */
+const char* cufk_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUFK_HIP_H */

@@ -1,0 +1,98 @@
+"""The C-ABI library loads on the host and exports every entry point include/cufk_hip.h
+declares; status paths that return before any device work behave as documented.  No kernel
+is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "cufk_hip.h"
+LIB = ROOT / "cufk_amd" / "libcufk_hip.so"
+
+OK, ERR_DTYPE, ERR_POINTS, ERR_SHAPE, ERR_STEPS, ERR_NULL, ERR_STRIDE = 0, 1, 2, 3, 4, 5, 6
+
+
+@pytest.fixture(scope="module")
+def lib():
+    lib = ctypes.CDLL(str(LIB))
+    i64, vp = ctypes.c_int64, ctypes.c_void_p
+    lib.cufk_reconstruct_fwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_bwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
+    lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
+    lib.cufk_error_string.restype = ctypes.c_char_p
+    lib.cufk_version.restype = ctypes.c_char_p
+    return lib
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cufk_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == [
+        "cufk_error_string",
+        "cufk_max_steps",
+        "cufk_reconstruct_bwd",
+        "cufk_reconstruct_fwd",
+        "cufk_torsion_bwd",
+        "cufk_torsion_fwd",
+        "cufk_version",
+    ]
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_status_strings(lib):
+    assert lib.cufk_error_string(OK) == b"success"
+    assert lib.cufk_error_string(ERR_POINTS) == b"point_count must be >= 4"
+    assert lib.cufk_error_string(ERR_SHAPE) == b"shape exceeds int32 kernel limits"
+    assert lib.cufk_error_string(ERR_DTYPE) == b"unsupported dtype"
+    assert lib.cufk_error_string(999) == b"unknown status"
+    assert lib.cufk_version() == b"0.1.0"
+
+
+def test_max_steps(lib):
+    for dtype in range(4):
+        assert lib.cufk_max_steps(dtype, 0, 0) == 2048
+        assert lib.cufk_max_steps(dtype, 1, 0) == 2048
+    assert lib.cufk_max_steps(9, 0, 0) == -ERR_DTYPE
+
+
+def test_reconstruct_status_paths(lib):
+    p = ctypes.c_void_p(1)  # never dereferenced: every call below returns before device work
+    null = None
+    f = lib.cufk_reconstruct_fwd
+    assert f(9, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(0, p, p, p, p, p, p, p, 4, 3, null) == ERR_POINTS
+    assert f(0, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert f(0, p, p, p, p, p, p, p, -1, 10, null) == ERR_SHAPE
+    assert f(0, p, p, p, p, p, p, p, 2**31, 10, null) == ERR_SHAPE
+    assert f(0, p, p, p, p, p, p, p, 0, 10, null) == OK  # empty batch: nothing to launch
+    assert f(0, null, p, p, p, p, p, p, 4, 10, null) == ERR_NULL
+    b = lib.cufk_reconstruct_bwd
+    assert b(0, p, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert b(0, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL
+    assert b(0, p, p, p, p, p, p, p, p, p, p, 0, 10, null) == OK
+
+
+def test_torsion_status_paths(lib):
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_torsion_fwd
+    assert f(0, p, 14, null, p, 2, 10, null) == ERR_NULL  # constants are required
+    assert f(0, p, -1, p, p, 2, 10, null) == ERR_STRIDE
+    assert f(0, p, 14, p, p, 2, 2052, null) == ERR_STEPS
+    assert f(0, p, 14, p, p, 0, 10, null) == OK
+    b = lib.cufk_torsion_bwd
+    assert b(0, p, 14, p, p, p, -3, p, 2, 10, null) == ERR_STRIDE
+    assert b(3, p, 14, p, p, p, 14, p, 2, 3, null) == ERR_POINTS

@@ -1,0 +1,322 @@
+"""GPU parity of the HIP path (through cufk_amd._C -> libcufk_hip.so) against the float64 oracle.
+
+Tolerances (stated per test):
+* float64 coordinates: max |x - oracle| <= 1e-12 * max(1, |x|) (reference-convention scan, fp64).
+* float32 coordinates at N = 2049: RMS <= 1e-5 nm and max-abs <= 1e-4 nm against float64
+  evaluated on the same (float32-valued) inputs.
+* float64 gradients: torch.autograd.gradcheck, and max |g - oracle| <= 1e-9 * max|oracle|.
+* float32 gradients: max |g - oracle| <= 2e-4 * max|oracle| per output (normwise).
+* float16 / bfloat16: errors are reported, not gated (finite outputs are required).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nerf64 as o
+
+pytestmark = pytest.mark.gpu
+
+BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
+BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
+
+
+@pytest.fixture(scope="module")
+def cufk(device):
+    import cufk_amd
+
+    return cufk_amd
+
+
+def _dev(x, dtype, device, requires_grad=False):
+    t = torch.as_tensor(np.asarray(x), dtype=torch.float64).to(device=device, dtype=dtype)
+    return t.requires_grad_(requires_grad)
+
+
+def _round(x, dtype):
+    """The values a `dtype` tensor holds, as float64 (the oracle consumes exactly these)."""
+    return torch.as_tensor(np.asarray(x), dtype=torch.float64).to(dtype).double().numpy()
+
+
+def _inputs(B, N, seed, anchors, dtype=torch.float64):
+    d = o.synthetic_inputs(B, N, seed, anchors=anchors)
+    return {k: _round(v, dtype) for k, v in d.items()}
+
+
+def _anchor_tensors(d, dtype, device):
+    if "p0" not in d:
+        return {}
+    return {k: _dev(d[k], dtype, device) for k in ("p0", "first_direction", "initial_normal")}
+
+
+def _anchor_np(d):
+    return {k: d.get(k) for k in ("p0", "first_direction", "initial_normal")}
+
+
+def _run(cufk, d, dtype, device, grad=True):
+    L = _dev(d["lengths"], dtype, device, grad)
+    A = _dev(d["angles"], dtype, device, grad)
+    D = _dev(d["dihedrals"], dtype, device, grad)
+    xyz = cufk.reconstruct(L, A, D, **_anchor_tensors(d, dtype, device))
+    if not grad:
+        return xyz, None
+    g = _dev(d["grad"], dtype, device)
+    grads = torch.autograd.grad(xyz, (L, A, D), g)
+    return xyz, grads
+
+
+# ----------------------------------------------------------------- forward
+
+
+@pytest.mark.parametrize("N", [4, 5, 6, 37, 64, 259, 260, 515, 516, 1027, 1028, 2051])
+@pytest.mark.parametrize("anchors", [False, True])
+def test_forward_fp64_matches_oracle(cufk, device, N, anchors):
+    d = _inputs(3, N, seed=N, anchors=anchors)
+    xyz, _ = _run(cufk, d, torch.float64, device, grad=False)
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    got = xyz.cpu().numpy()
+    err = np.abs(got - ref).max()
+    print(f"fp64 forward N={N} anchors={anchors}: max err {err:.3e}")
+    assert err <= 1e-12 * max(1.0, np.abs(ref).max())
+
+
+def test_forward_fp32_tolerance_at_cap(cufk, device):
+    # Config 2 shape per chain (N = 2049) with explicit random anchors; 32 chains.
+    d = _inputs(32, 2049, seed=2, anchors=True, dtype=torch.float32)
+    xyz, _ = _run(cufk, d, torch.float32, device, grad=False)
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    diff = xyz.double().cpu().numpy() - ref
+    rms = math.sqrt(np.mean(np.sum(diff**2, axis=-1)))
+    mx = np.abs(diff).max()
+    print(f"fp32 forward N=2049: rms {rms:.3e} nm, max {mx:.3e} nm")
+    assert rms <= 1e-5
+    assert mx <= 1e-4
+
+
+def test_forward_golden_fixture(cufk, device, golden_c0):
+    g = golden_c0
+    for dtype, tol in ((torch.float64, 1e-13), (torch.float32, 2e-6)):
+        L = _dev(g["lengths"], dtype, device)
+        A = _dev(g["angles"], dtype, device)
+        D = _dev(g["dihedrals"], dtype, device)
+        xyz = cufk.reconstruct(L, A, D)
+        assert xyz.shape == g["xyz"].shape
+        err = np.abs(xyz.double().cpu().numpy() - g["xyz"]).max()
+        print(f"golden C0 {dtype}: max err {err:.3e}")
+        assert err <= tol
+
+
+def test_single_chain_shapes(cufk, device):
+    d = _inputs(1, 20, seed=5, anchors=False)
+    L = _dev(d["lengths"][0], torch.float32, device, True)
+    A = _dev(d["angles"][0], torch.float32, device, True)
+    D = _dev(d["dihedrals"][0], torch.float32, device, True)
+    xyz = cufk.reconstruct(L, A, D)
+    assert xyz.shape == (20, 3) and xyz.dtype == torch.float32
+    gl, ga, gd = torch.autograd.grad(xyz, (L, A, D), torch.ones_like(xyz))
+    assert gl.shape == (19,) and ga.shape == (18,) and gd.shape == (17,)
+
+
+def test_noncontiguous_inputs(cufk, device):
+    d = _inputs(4, 50, seed=9, anchors=False)
+    wide = {k: np.concatenate([d[k], d[k]], axis=1) for k in ("lengths", "angles", "dihedrals")}
+    L = _dev(wide["lengths"], torch.float64, device)[:, : d["lengths"].shape[1]]
+    A = _dev(wide["angles"], torch.float64, device)[:, : d["angles"].shape[1]]
+    D = _dev(wide["dihedrals"], torch.float64, device)[:, : d["dihedrals"].shape[1]]
+    assert not L.is_contiguous()
+    xyz = cufk.reconstruct(L, A, D)
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"])
+    assert np.abs(xyz.cpu().numpy() - ref).max() <= 1e-12
+
+
+def test_empty_batch(cufk, device):
+    L = torch.zeros(0, 9, device=device)
+    xyz = cufk.reconstruct(L, torch.zeros(0, 8, device=device), torch.zeros(0, 7, device=device))
+    assert xyz.shape == (0, 10, 3)
+
+
+# ----------------------------------------------------------------- backward
+
+
+@pytest.mark.parametrize("N", [4, 5, 9, 64, 259, 515, 1028, 2051])
+def test_backward_fp64_matches_oracle(cufk, device, N):
+    d = _inputs(2, N, seed=100 + N, anchors=True)
+    _, grads = _run(cufk, d, torch.float64, device)
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for name, got, want in zip(("lengths", "angles", "dihedrals"), grads, ref):
+        err = np.abs(got.cpu().numpy() - want).max()
+        scale = max(1.0, np.abs(want).max())
+        print(f"fp64 backward N={N} d/d{name}: max err {err:.3e} (scale {scale:.3e})")
+        assert err <= 1e-9 * scale
+
+
+def test_backward_degenerate_geometry_fp64(cufk, device):
+    # Negative lengths, angles outside (0, pi) and a first direction parallel to the normal:
+    # the exact-frame adjoint has no sign or degeneracy cases.
+    d = _inputs(2, 30, seed=11, anchors=False)
+    d["lengths"][:, 3] *= -1.0
+    d["angles"][:, 0] = -0.7
+    d["angles"][:, 5] = 3.5
+    d["p0"] = np.array([0.3, -0.2, 0.1])
+    d["first_direction"] = np.array([0.0, 0.0, 2.0])
+    d["initial_normal"] = np.array([0.0, 0.0, 1.0])
+    xyz, grads = _run(cufk, d, torch.float64, device)
+    ref_x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    assert np.abs(xyz.detach().cpu().numpy() - ref_x).max() <= 1e-12
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for got, want in zip(grads, ref):
+        assert np.abs(got.cpu().numpy() - want).max() <= 1e-9 * max(1.0, np.abs(want).max())
+
+
+def test_gradcheck_fp64(cufk, device):
+    d = _inputs(2, 12, seed=3, anchors=True)
+    L = _dev(d["lengths"], torch.float64, device, True)
+    A = _dev(d["angles"], torch.float64, device, True)
+    D = _dev(d["dihedrals"], torch.float64, device, True)
+    an = _anchor_tensors(d, torch.float64, device)
+    assert torch.autograd.gradcheck(lambda a, b, c: cufk.reconstruct(a, b, c, **an), (L, A, D), eps=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("N", [384, 2049])
+def test_backward_fp32_tolerance(cufk, device, N):
+    d = _inputs(8, N, seed=N, anchors=True, dtype=torch.float32)
+    _, grads = _run(cufk, d, torch.float32, device)
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for name, got, want in zip(("lengths", "angles", "dihedrals"), grads, ref):
+        err = np.abs(got.double().cpu().numpy() - want).max()
+        scale = np.abs(want).max()
+        print(f"fp32 backward N={N} d/d{name}: max err {err:.3e}, rel {err / scale:.3e}")
+        assert err <= 2e-4 * scale
+
+
+# ----------------------------------------------------------------- torsion
+
+
+@pytest.mark.parametrize("N", [4, 5, 6, 7, 100, 387, 388, 771, 772, 1539, 1540, 2051])
+def test_torsion_fp64_matches_oracle(cufk, device, N):
+    rng = np.random.default_rng(N)
+    B = 3
+    raw = rng.normal(size=(B, 2 * (N - 3)))
+    g = rng.normal(size=(B, N, 3))
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    r = _dev(raw, torch.float64, device, True)
+    xyz = f(r)
+    ref = o.torsion_forward(raw, consts)
+    err = np.abs(xyz.detach().cpu().numpy() - ref).max()
+    (graw,) = torch.autograd.grad(xyz, (r,), _dev(g, torch.float64, device))
+    ref_g = o.torsion_backward(raw, ref, g, consts)
+    gerr = np.abs(graw.cpu().numpy() - ref_g).max()
+    print(f"torsion fp64 N={N}: xyz err {err:.3e}, grad err {gerr:.3e}")
+    assert err <= 1e-12 * max(1.0, np.abs(ref).max())
+    assert gerr <= 1e-9 * max(1.0, np.abs(ref_g).max())
+
+
+def test_torsion_matches_reconstruct_fp64(cufk, device):
+    rng = np.random.default_rng(0)
+    B, N = 2, 301
+    raw = rng.normal(size=(B, 2 * (N - 3)))
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    xyz_t = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)(_dev(raw, torch.float64, device))
+    Sn, Cn, _ = o._normalize_pairs(raw)
+    L = np.array([consts.lengths[i % 3] for i in range(N - 1)])[None].repeat(B, 0)
+    A = np.array([math.atan2(consts.sin[i % 3], consts.cos[i % 3]) for i in range(N - 2)])[None].repeat(B, 0)
+    xyz_r = cufk.reconstruct(_dev(L, torch.float64, device), _dev(A, torch.float64, device), _dev(np.arctan2(Sn, Cn), torch.float64, device))
+    assert torch.allclose(xyz_t, xyz_r, atol=1e-12, rtol=0)
+
+
+def test_torsion_fp32_tolerance(cufk, device):
+    rng = np.random.default_rng(771)
+    B, N = 16, 771
+    raw = _round(rng.normal(size=(B, 2 * (N - 3))), torch.float32)
+    g = _round(rng.normal(size=(B, N, 3)), torch.float32)
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    r = _dev(raw, torch.float32, device, True)
+    xyz = f(r)
+    (graw,) = torch.autograd.grad(xyz, (r,), _dev(g, torch.float32, device))
+    ref = o.torsion_forward(raw, consts)
+    diff = xyz.detach().double().cpu().numpy() - ref
+    rms = math.sqrt(np.mean(np.sum(diff**2, -1)))
+    ref_g = o.torsion_backward(raw, ref, g, consts)
+    gerr = np.abs(graw.double().cpu().numpy() - ref_g).max() / np.abs(ref_g).max()
+    print(f"torsion fp32 N={N}: rms {rms:.3e}, max {np.abs(diff).max():.3e}, grad rel {gerr:.3e}")
+    assert rms <= 1e-5 and np.abs(diff).max() <= 1e-4
+    assert gerr <= 2e-4
+
+
+def test_torsion_strided_rows_keep_grad_strides(cufk, device):
+    rng = np.random.default_rng(5)
+    B, N = 4, 40
+    wide = rng.normal(size=(B, 2 * (N - 3) + 6))
+    base = _dev(wide, torch.float64, device)
+    raw = base[:, 2 : 2 + 2 * (N - 3)].detach().requires_grad_(False)
+    raw = base[:, 2 : 2 + 2 * (N - 3)]
+    assert raw.stride(0) == wide.shape[1] and not raw.is_contiguous()
+    leaf = raw.detach().clone().requires_grad_(True)
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    xyz = f(raw.detach())  # strided, no grad
+    ref = o.torsion_forward(wide[:, 2 : 2 + 2 * (N - 3)], consts)
+    assert np.abs(xyz.cpu().numpy() - ref).max() <= 1e-12
+    # Gradient of a strided input: autograd hands back the kernel's stride-preserving tensor.
+    strided = base.detach().clone()[:, 2 : 2 + 2 * (N - 3)].requires_grad_(True)
+    out = f(strided)
+    g = rng.normal(size=(B, N, 3))
+    (gr,) = torch.autograd.grad(out, (strided,), _dev(g, torch.float64, device))
+    ref_g = o.torsion_backward(wide[:, 2 : 2 + 2 * (N - 3)], ref, g, consts)
+    assert np.abs(gr.cpu().numpy() - ref_g).max() <= 1e-9 * np.abs(ref_g).max()
+    del leaf
+
+
+# ----------------------------------------------------------------- low precision (reported)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_low_precision_reported(cufk, device, dtype):
+    d = _inputs(8, 1026, seed=4, anchors=False, dtype=dtype)
+    xyz, grads = _run(cufk, d, dtype, device)
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"])
+    diff = xyz.detach().double().cpu().numpy() - ref
+    err_pos = np.sqrt(np.mean(np.sum(diff**2, -1), axis=0))
+    print(f"{dtype} forward N=1026: rms {math.sqrt(np.mean(err_pos**2)):.3e}, max {np.abs(diff).max():.3e}, "
+          f"rms at positions 10/100/1000: {err_pos[10]:.2e}/{err_pos[100]:.2e}/{err_pos[1000]:.2e}")
+    assert torch.isfinite(xyz).all()
+    for gr in grads:
+        assert torch.isfinite(gr).all()
+
+
+# ----------------------------------------------------------------- runtime behaviour
+
+
+def test_deterministic_and_stream(cufk, device):
+    d = _inputs(64, 700, seed=8, anchors=True, dtype=torch.float32)
+    x1, g1 = _run(cufk, d, torch.float32, device)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        x2, g2 = _run(cufk, d, torch.float32, device)
+    s.synchronize()
+    assert torch.equal(x1, x2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_full_size_config2_sampled(cufk, device):
+    # B = 4096, N = 2049 fp32: compare 6 sampled chains with the float64 oracle.
+    B, N = 4096, 2049
+    d = _inputs(B, N, seed=2, anchors=True, dtype=torch.float32)
+    xyz, grads = _run(cufk, d, torch.float32, device)
+    torch.cuda.synchronize()
+    idx = [0, 1, 1000, 2047, 4000, 4095]
+    sub = {k: (v[idx] if k in ("lengths", "angles", "dihedrals", "grad") else v) for k, v in d.items()}
+    ref = o.reconstruct_forward(sub["lengths"], sub["angles"], sub["dihedrals"], **_anchor_np(sub))
+    diff = xyz.detach()[idx].double().cpu().numpy() - ref
+    rms = math.sqrt(np.mean(np.sum(diff**2, -1)))
+    assert rms <= 1e-5 and np.abs(diff).max() <= 1e-4
+    ref_g = o.reconstruct_backward(sub["lengths"], sub["angles"], sub["dihedrals"], sub["grad"], **_anchor_np(sub))
+    for got, want in zip(grads, ref_g):
+        assert np.abs(got[idx].double().cpu().numpy() - want).max() <= 2e-4 * np.abs(want).max()

@@ -1,0 +1,303 @@
+"""Pins for the float64 oracle (CPU only).
+
+Each oracle function is checked against something other than its own formula: an
+independent algorithm (serial Parsons NeRF, torch autograd through that NeRF, finite
+differences, the chain rule through atan2), an invariant (internal-coordinate round trip,
+rigid-motion covariance), or a closed form.  The mutation tests at the end plant plausible
+mistakes in copies of the oracle and show that these checks catch them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nerf64 as o
+
+BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
+BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
+
+
+def _anchors(d):
+    return dict(p0=d["p0"], first_direction=d["first_direction"], initial_normal=d["initial_normal"])
+
+
+def _wrap(a):
+    return np.angle(np.exp(1j * a))
+
+
+# ------------------------------------------------------------------ forward
+
+
+@pytest.mark.parametrize("N", [4, 5, 17, 64, 300])
+@pytest.mark.parametrize("anchors", [False, True])
+def test_forward_equals_serial_nerf(N, anchors):
+    d = o.synthetic_inputs(3, N, seed=N, anchors=anchors)
+    an = _anchors(d) if anchors else {}
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+    y = o.nerf_serial(d["lengths"], d["angles"], d["dihedrals"], **an)
+    assert np.abs(x - y).max() < 1e-12
+
+
+@pytest.mark.parametrize("N", [4, 40, 500])
+def test_internal_coordinate_round_trip(N):
+    d = o.synthetic_inputs(2, N, seed=1, anchors=True)
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchors(d))
+    L, A, D = o.measure_internal(x)
+    assert np.abs(L - d["lengths"]).max() < 1e-12
+    assert np.abs(A - d["angles"]).max() < 1e-11
+    # IUPAC sign convention: atan2(|b2| b1.(b2 x b3), (b1 x b2).(b2 x b3)).
+    assert np.abs(_wrap(D - d["dihedrals"])).max() < 1e-11
+
+
+def test_default_frame_closed_form():
+    d = o.synthetic_inputs(4, 10, seed=3, anchors=False)
+    L, A = d["lengths"], d["angles"]
+    x = o.reconstruct_forward(L, A, d["dihedrals"])
+    assert np.abs(x[:, 0]).max() == 0.0
+    np.testing.assert_allclose(x[:, 1], np.stack([L[:, 0], 0 * L[:, 0], 0 * L[:, 0]], -1), atol=1e-15)
+    x2 = np.stack([L[:, 0] - L[:, 1] * np.cos(A[:, 0]), L[:, 1] * np.sin(A[:, 0]), 0 * L[:, 0]], -1)
+    np.testing.assert_allclose(x[:, 2], x2, atol=1e-15)
+
+
+def test_anchor_covariance():
+    d = o.synthetic_inputs(3, 50, seed=4, anchors=True)
+    x0 = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"])
+    # Unnormalised anchors: the oracle must normalise and Gram-Schmidt them.
+    fd = 3.0 * d["first_direction"]
+    n0 = 0.5 * d["initial_normal"] + 0.7 * d["first_direction"]
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], p0=d["p0"], first_direction=fd, initial_normal=n0)
+    dh = fd / np.linalg.norm(fd)
+    nh = n0 - (n0 @ dh) * dh
+    nh /= np.linalg.norm(nh)
+    R = np.stack([dh, np.cross(nh, dh), nh], axis=-1)
+    np.testing.assert_allclose(x, d["p0"] + x0 @ R.T, atol=1e-13)
+
+
+@pytest.mark.parametrize("fd", [(0.0, 0.0, 1.0), (1.0, 0.0, 0.0), (0.95, 0.1, 0.0)])
+def test_degenerate_normal_uses_stable_perpendicular(fd):
+    # initial_normal parallel to first_direction: block.cu:126 falls back to
+    # normalized(d0 x helper), helper = e_x unless |d0_x| >= 0.9 (frame_utils.cuh:23-31).
+    d = o.synthetic_inputs(1, 8, seed=5, anchors=False)
+    fd = np.array(fd)
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], first_direction=fd, initial_normal=2 * fd)
+    dh = fd / np.linalg.norm(fd)
+    helper = np.array([0.0, 1.0, 0.0]) if abs(dh[0]) >= 0.9 else np.array([1.0, 0.0, 0.0])
+    nh = np.cross(dh, helper)
+    nh /= np.linalg.norm(nh)
+    th = np.cross(nh, dh)
+    a0, l1 = d["angles"][0, 0], d["lengths"][0, 1]
+    x2 = d["lengths"][0, 0] * dh + l1 * (-math.cos(a0) * dh + math.sin(a0) * th)
+    np.testing.assert_allclose(x[0, 2], x2, atol=1e-15)
+
+
+# ------------------------------------------------------------------ backward
+
+
+def _torch_nerf(L, A, D):
+    """Serial NeRF in torch (independent of the oracle's affine scan), default anchors."""
+    B = L.shape[0]
+    z = torch.zeros(B, dtype=L.dtype)
+    pts = [torch.zeros(B, 3, dtype=L.dtype), torch.stack([L[:, 0], z, z], -1)]
+    pts.append(torch.stack([L[:, 0] - L[:, 1] * torch.cos(A[:, 0]), L[:, 1] * torch.sin(A[:, 0]), z], -1))
+    for k in range(D.shape[1]):
+        a, b, c = pts[k], pts[k + 1], pts[k + 2]
+        bc = (c - b) / torch.linalg.norm(c - b, dim=-1, keepdim=True)
+        n = torch.cross(b - a, bc, dim=-1)
+        n = n / torch.linalg.norm(n, dim=-1, keepdim=True)
+        m = torch.stack([bc, torch.cross(n, bc, dim=-1), n], -1)
+        l, t, p = L[:, k + 2], A[:, k + 1], D[:, k]
+        d2 = torch.stack([-l * torch.cos(t), l * torch.sin(t) * torch.cos(p), l * torch.sin(t) * torch.sin(p)], -1)
+        pts.append(c + torch.einsum("bij,bj->bi", m, d2))
+    return torch.stack(pts, 1)
+
+
+@pytest.mark.parametrize("N", [4, 6, 25])
+def test_backward_matches_torch_autograd_of_serial_nerf(N):
+    d = o.synthetic_inputs(3, N, seed=20 + N, anchors=False)
+    L, A, D = (torch.tensor(d[k], requires_grad=True) for k in ("lengths", "angles", "dihedrals"))
+    x = _torch_nerf(L, A, D)
+    gt = torch.autograd.grad(x, (L, A, D), torch.tensor(d["grad"]))
+    go = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    for a, b in zip(gt, go):
+        assert np.abs(a.numpy() - b).max() < 1e-12
+
+
+def test_backward_matches_finite_differences_with_anchors():
+    d = o.synthetic_inputs(1, 14, seed=6, anchors=True)
+    an = _anchors(d)
+    g = d["grad"]
+    grads = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], g, **an)
+    h = 1e-6
+    for idx, key in enumerate(("lengths", "angles", "dihedrals")):
+        fd = np.zeros_like(d[key])
+        for j in range(d[key].shape[1]):
+            plus = {k: d[k].copy() for k in ("lengths", "angles", "dihedrals")}
+            minus = {k: d[k].copy() for k in ("lengths", "angles", "dihedrals")}
+            plus[key][0, j] += h
+            minus[key][0, j] -= h
+            fp = np.sum(o.reconstruct_forward(plus["lengths"], plus["angles"], plus["dihedrals"], **an) * g)
+            fm = np.sum(o.reconstruct_forward(minus["lengths"], minus["angles"], minus["dihedrals"], **an) * g)
+            fd[0, j] = (fp - fm) / (2 * h)
+        assert np.abs(fd - grads[idx]).max() < 1e-7
+
+
+def test_adjoint_forms_agree():
+    d = o.synthetic_inputs(3, 60, seed=7, anchors=True)
+    args = (d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    ref = o.reconstruct_backward(*args, **_anchors(d))
+    world = o.reconstruct_backward_world(*args, **_anchors(d))
+    frames = o.reconstruct_backward_frames(*args, **_anchors(d))
+    for a, b, c in zip(ref, world, frames):
+        assert np.abs(a - b).max() < 1e-12 * max(1, np.abs(a).max())
+        assert np.abs(a - c).max() < 1e-12 * max(1, np.abs(a).max())
+
+
+def test_frame_adjoint_handles_signs_the_world_form_cannot():
+    d = o.synthetic_inputs(2, 20, seed=8, anchors=True)
+    d["lengths"][:, 4] *= -1
+    d["angles"][:, 0] = -0.6
+    d["angles"][:, 6] = 3.6
+    args = (d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    ref = o.reconstruct_backward(*args, **_anchors(d))
+    frames = o.reconstruct_backward_frames(*args, **_anchors(d))
+    world = o.reconstruct_backward_world(*args, **_anchors(d))
+    for a, c in zip(ref, frames):
+        assert np.abs(a - c).max() < 1e-12 * max(1, np.abs(a).max())
+    assert max(np.abs(a - w).max() for a, w in zip(ref, world)) > 1e-3
+
+
+# ------------------------------------------------------------------ torsion
+
+
+def test_torsion_constants_closed_form():
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    assert c.lengths == tuple(float(np.float32(v)) for v in BOND_LENGTHS)
+    assert c.sin == tuple(math.sin(a) for a in BOND_ANGLES)
+    assert c.cos == tuple(math.cos(a) for a in BOND_ANGLES)
+    with pytest.raises(AssertionError):
+        o.torsion_constants((1.0, 2.0), BOND_ANGLES)
+
+
+def _tiled(c, B, N):
+    L = np.array([c.lengths[i % 3] for i in range(N - 1)])[None].repeat(B, 0)
+    A = np.array([math.atan2(c.sin[i % 3], c.cos[i % 3]) for i in range(N - 2)])[None].repeat(B, 0)
+    return L, A
+
+
+@pytest.mark.parametrize("N", [4, 5, 6, 47])
+def test_torsion_equals_reconstruct_with_tiled_constants(N):
+    rng = np.random.default_rng(N)
+    raw = rng.normal(size=(2, 2 * (N - 3)))
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    L, A = _tiled(c, 2, N)
+    D = np.arctan2(raw[:, 0::2], raw[:, 1::2])
+    np.testing.assert_allclose(o.torsion_forward(raw, c), o.reconstruct_forward(L, A, D), atol=1e-14)
+
+
+def test_torsion_backward_is_chain_rule_through_atan2():
+    rng = np.random.default_rng(9)
+    B, N = 2, 31
+    raw = rng.normal(size=(B, 2 * (N - 3)))
+    g = rng.normal(size=(B, N, 3))
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    L, A = _tiled(c, B, N)
+    rs, rc = raw[:, 0::2], raw[:, 1::2]
+    _, _, gD = o.reconstruct_backward(L, A, np.arctan2(rs, rc), g)
+    n2 = rs * rs + rc * rc
+    expect = np.empty_like(raw)
+    expect[:, 0::2] = gD * rc / n2
+    expect[:, 1::2] = -gD * rs / n2
+    got = o.torsion_backward(raw, o.torsion_forward(raw, c), g, c)
+    # 1/l is formed in float (torsion.cu:216): relative differences ~1e-8 are expected.
+    assert np.abs(got - expect).max() <= 1e-7 * np.abs(expect).max()
+
+
+def test_torsion_backward_finite_differences():
+    rng = np.random.default_rng(10)
+    raw = rng.normal(size=(1, 2 * 9))
+    g = rng.normal(size=(1, 12, 3))
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    got = o.torsion_backward(raw, o.torsion_forward(raw, c), g, c)
+    h = 1e-6
+    fd = np.zeros_like(raw)
+    for j in range(raw.shape[1]):
+        p, m = raw.copy(), raw.copy()
+        p[0, j] += h
+        m[0, j] -= h
+        fd[0, j] = (np.sum(o.torsion_forward(p, c) * g) - np.sum(o.torsion_forward(m, c) * g)) / (2 * h)
+    assert np.abs(fd - got).max() < 1e-6 * max(1, np.abs(got).max())
+
+
+def test_torsion_clamps_tiny_pairs():
+    raw = np.zeros((1, 6))
+    raw[0, 2:4] = (1e-10, -2e-10)
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    S, C, n2 = o._normalize_pairs(raw)
+    assert n2[0, 0] == o.K_NORM_EPS2 and S[0, 0] == 0.0 and C[0, 0] == 0.0
+    assert np.all(np.isfinite(o.torsion_forward(raw, c)))
+
+
+# ------------------------------------------------------------------ golden fixtures (regression)
+
+
+def test_golden_c0_regenerates(golden_c0):
+    g = golden_c0
+    np.testing.assert_array_equal(o.reconstruct_forward(g["lengths"], g["angles"], g["dihedrals"]), g["xyz"])
+    gL, gA, gD = o.reconstruct_backward(g["lengths"], g["angles"], g["dihedrals"], g["grad"])
+    np.testing.assert_array_equal(gL, g["grad_lengths"])
+    np.testing.assert_array_equal(gD, g["grad_dihedrals"])
+    L, A, D = o.measure_internal(g["xyz"])
+    assert np.abs(_wrap(D - g["dihedrals"])).max() < 1e-11
+
+
+def test_golden_anchored_regenerates(golden_anchored):
+    g = golden_anchored
+    an = dict(p0=g["p0"], first_direction=g["first_direction"], initial_normal=g["initial_normal"])
+    np.testing.assert_allclose(o.reconstruct_forward(g["lengths"], g["angles"], g["dihedrals"], **an), g["xyz"], atol=0)
+    np.testing.assert_allclose(o.nerf_serial(g["lengths"], g["angles"], g["dihedrals"], **an), g["xyz"], atol=1e-13)
+
+
+def test_golden_torsion_regenerates(golden_torsion):
+    g = golden_torsion
+    c = o.torsion_constants(tuple(g["bond_lengths"]), tuple(g["bond_angles"]))
+    np.testing.assert_array_equal(o.torsion_forward(g["raw_pairs"], c), g["xyz"])
+    np.testing.assert_array_equal(o.torsion_backward(g["raw_pairs"], g["xyz"], g["grad"], c), g["grad_raw"])
+
+
+# ------------------------------------------------------------------ planted mistakes
+
+
+def test_checks_catch_a_flipped_dihedral_sign(monkeypatch):
+    real = o.local_transform
+    monkeypatch.setattr(o, "local_transform", lambda l, t, p: real(l, t, -p))
+    d = o.synthetic_inputs(1, 30, seed=11, anchors=False)
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"])
+    _, _, D = o.measure_internal(x)
+    assert np.abs(_wrap(D - d["dihedrals"])).max() > 1e-3
+    assert np.abs(x - o.nerf_serial(d["lengths"], d["angles"], d["dihedrals"])).max() > 1e-3
+
+
+def test_checks_catch_a_transposed_compose(monkeypatch):
+    monkeypatch.setattr(o, "_compose", lambda am, av, bm, bv: (bm @ am, bv + np.einsum("bij,bj->bi", bm, av)))
+    d = o.synthetic_inputs(1, 30, seed=12, anchors=False)
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"])
+    assert np.abs(x - o.nerf_serial(d["lengths"], d["angles"], d["dihedrals"])).max() > 1e-3
+
+
+def test_checks_catch_a_dropped_first_frame_gradient_term():
+    d = o.synthetic_inputs(2, 12, seed=13, anchors=False)
+    gL, gA, gD = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    L, A, D = (torch.tensor(d[k], requires_grad=True) for k in ("lengths", "angles", "dihedrals"))
+    tA = torch.autograd.grad(_torch_nerf(L, A, D), (A,), torch.tensor(d["grad"]))[0].numpy()
+    # Dropping the l1 * grad_p2 . d_dir term of block.cu:227 breaks agreement with autograd.
+    ff = o.first_frame(d["lengths"][:, 0], d["lengths"][:, 1], d["angles"][:, 0], (0, 0, 0), (1, 0, 0), (0, 0, 1))
+    s, c = np.sin(d["angles"][:, 0]), np.cos(d["angles"][:, 0])
+    d_dir = s[:, None] * ff.dir0 + c[:, None] * ff.turn0
+    F2 = d["grad"][:, 2:].sum(1)
+    dropped = gA[:, 0] - d["lengths"][:, 1] * np.sum(F2 * d_dir, -1)
+    assert np.abs(gA[:, 0] - tA[:, 0]).max() < 1e-12
+    assert np.abs(dropped - tA[:, 0]).max() > 1e-3
