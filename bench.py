@@ -54,7 +54,24 @@ def parse_args():
     p.add_argument("--kernel-reps", type=int, default=50)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = auto)")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     return p.parse_args()
+
+
+def copy_probe(mib):
+    """A plain copy kernel of known size: reads and writes exactly mib MiB once per launch."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = event_time_ms(torch, lambda: dst.copy_(src), 10)
+    print(json.dumps({"copy_probe_mib": mib, "avg_us": ms * 1e3, "GBs_read_plus_write": 2 * n * 4 / (ms * 1e-3) / 1e9}))
+    return 0
 
 
 def synthetic(B, N, seed, torch, device, dtype):
@@ -117,6 +134,9 @@ def main():
         )
         return 2
 
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
+
     import torch
 
     import cufk_amd
@@ -173,15 +193,19 @@ def main():
     i64 = ctypes.c_int64
     if kind == "reconstruct":
         xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+        regular = torch.empty(B, device=device, dtype=torch.uint8)
         gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
 
+        # The entry points the autograd path uses: the flagged forward and the backward that
+        # takes the forward's output (position-based adjoint for regular chains).
         def fwd():
-            rc = lib.cufk_reconstruct_fwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), i64(B), i64(N), st)
+            rc = lib.cufk_reconstruct_fwd_flagged(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(regular),
+                                                  i64(B), i64(N), st)
             assert rc == 0, rc
 
         def bwd():
-            rc = lib.cufk_reconstruct_bwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(g), P(gL), P(gA), P(gD),
-                                          i64(B), i64(N), st)
+            rc = lib.cufk_reconstruct_bwd_saved(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(regular), P(g),
+                                                P(gL), P(gA), P(gD), i64(B), i64(N), st)
             assert rc == 0, rc
     else:
         import math
@@ -205,6 +229,7 @@ def main():
 
     t_fwd = event_time_ms(torch, fwd, args.kernel_reps)
     t_bwd = event_time_ms(torch, bwd, args.kernel_reps)
+    regular_frac = float(regular.float().mean()) if kind == "reconstruct" else None
 
     atoms = B * N
     bw_bwd = bwd_bytes / (t_bwd * 1e-3) / 1e9
@@ -242,6 +267,7 @@ def main():
             "fwd_plus_bwd_us": (t_fwd + t_bwd) * 1e3,
             "fwd_plus_bwd_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / ((t_fwd + t_bwd) * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "fwd_plus_bwd_atoms_per_s": atoms / ((t_fwd + t_bwd) * 1e-3),
+            "regular_chain_fraction": regular_frac,
         },
     }
     if not args.no_cpu_baseline:

@@ -32,7 +32,7 @@ EXT_LIB = PKG / f"_C{EXT_SUFFIX}"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-Xclang",
     "-target-feature",

@@ -144,11 +144,21 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     const c10::DeviceGuard guard(lengths.device());
     check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
     Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
-    check_status(cufk_reconstruct_fwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
-                                      a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
-                                      xyz.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
-                 "cufk_reconstruct_fwd");
+    Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
+    check_status(cufk_reconstruct_fwd_flagged(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                              dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                              a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                              static_cast<uint8_t*>(regular.data_ptr()), shape.batch, shape.points,
+                                              current_stream(lengths)),
+                 "cufk_reconstruct_fwd_flagged");
+    // The reference saves only the inputs (block.cu:408).  The output is kept as a detached
+    // alias (no grad_fn, so no reference cycle; it shares the output's version counter): when
+    // it is untouched at backward time, regular chains use the position-based adjoint;
+    // if the caller modified it in place, every chain takes the exact recompute.
     ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
+    ctx->saved_data["xyz"] = xyz.detach();
+    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["regular"] = regular;
     return xyz;
   }
 
@@ -171,11 +181,23 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     Tensor grad_lengths = torch::empty_like(lengths);
     Tensor grad_angles = torch::empty_like(angles);
     Tensor grad_dihedrals = torch::empty_like(dihedrals);
-    check_status(cufk_reconstruct_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
-                                      a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
-                                      grad_points.data_ptr(), grad_lengths.data_ptr(), grad_angles.data_ptr(),
-                                      grad_dihedrals.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
-                 "cufk_reconstruct_bwd");
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    const Tensor regular = ctx->saved_data["regular"].toTensor();
+    if (xyz._version() == ctx->saved_data["xyz_version"].toInt()) {
+      check_status(cufk_reconstruct_bwd_saved(
+                       dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(),
+                       a.first_direction.data_ptr(), a.initial_normal.data_ptr(), xyz.data_ptr(),
+                       static_cast<const uint8_t*>(regular.data_ptr()), grad_points.data_ptr(), grad_lengths.data_ptr(),
+                       grad_angles.data_ptr(), grad_dihedrals.data_ptr(), shape.batch, shape.points,
+                       current_stream(lengths)),
+                   "cufk_reconstruct_bwd_saved");
+    } else {
+      check_status(cufk_reconstruct_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
+                                        a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
+                                        grad_points.data_ptr(), grad_lengths.data_ptr(), grad_angles.data_ptr(),
+                                        grad_dihedrals.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
+                   "cufk_reconstruct_bwd");
+    }
     return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor()};
   }
 };

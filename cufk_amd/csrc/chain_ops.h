@@ -83,6 +83,8 @@ template <typename R> __device__ __forceinline__ void pair_unit(R rs, R rc, doub
 
 __device__ __forceinline__ float sqrt_r(float x) { return sqrtf(x); }
 __device__ __forceinline__ double sqrt_r(double x) { return sqrt(x); }
+__device__ __forceinline__ float rsqrt_r(float x) { return rsqrtf(x); }
+__device__ __forceinline__ double rsqrt_r(double x) { return rsqrt(x); }
 
 // ------------------------------------------------------------------ small vectors
 
@@ -187,6 +189,7 @@ __device__ __forceinline__ void step_backward(R (&m)[9], R s, R c, R S, R C) {
 template <typename R> struct FirstFrame {
   V3<R> p0, p1, p2, d0, t0, d1;
   R frame[9];  // row-major
+  R L0, L1, sinA0;
 };
 
 template <typename T>
@@ -211,6 +214,9 @@ __device__ __forceinline__ FirstFrame<compute_t<T>> first_frame(compute_t<T> L0,
   double sd, cd;
   sin_cos_wide(A0, sd, cd);
   const R s = static_cast<R>(sd), c = static_cast<R>(cd);
+  f.L0 = L0;
+  f.L1 = L1;
+  f.sinA0 = s;
   f.d1 = (-c) * f.d0 + s * f.t0;
   f.p2 = f.p1 + L1 * f.d1;
   const V3<R> n = normalized(cross(f.d0, f.d1));
@@ -304,6 +310,20 @@ template <typename R> __device__ __forceinline__ ForceMoment<R> wave_suffix(Forc
   return a;
 }
 
+template <typename R> __device__ __forceinline__ R wave_min(R x) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x = fmin(x, __shfl_xor(x, d));
+  return x;
+}
+
+template <typename R> __device__ __forceinline__ R wave_max(R x) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x = fmax(x, __shfl_xor(x, d));
+  return x;
+}
+
+template <typename R> __device__ __forceinline__ V3<R> load3(const R* p) { return {p[0], p[1], p[2]}; }
+
 template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(const ForceMoment<R>& a, int lane) {
   ForceMoment<R> b;
   b.f.x = shfl_down_or_zero(a.f.x, 1, lane);
@@ -313,6 +333,71 @@ template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(
   b.m.y = shfl_down_or_zero(a.m.y, 1, lane);
   b.m.z = shfl_down_or_zero(a.m.z, 1, lane);
   return b;
+}
+
+// ------------------------------------------------------------------ workgroup scans
+
+template <typename R, int W>
+__device__ __forceinline__ void store_rigid(R (&dst)[W][12], int w, const Rigid<R>& a) {
+#pragma unroll
+  for (int i = 0; i < 9; ++i) dst[w][i] = a.m[i];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) dst[w][9 + i] = a.v[i];
+}
+
+template <typename R, int W>
+__device__ __forceinline__ Rigid<R> load_rigid(const R (&src)[W][12], int w) {
+  Rigid<R> a;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) a.m[i] = src[w][i];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) a.v[i] = src[w][9 + i];
+  return a;
+}
+
+// Exclusive prefix of the chain's rigid transforms before this lane's first step:
+// wave-level scan, then the totals of earlier waves (scan.cuh:63-101 restated for wave64).
+// Contains one __syncthreads(); must be called by every thread of the workgroup.
+template <typename R, int W>
+__device__ __forceinline__ Rigid<R> lane_carry(const Rigid<R>& lane_total, R (&wave_total)[W][12], int lane, int wave) {
+  const Rigid<R> incl = wave_prefix(lane_total);
+  if (lane == 63) store_rigid(wave_total, wave, incl);
+  Rigid<R> excl = wave_shift_up(incl, lane);
+  __syncthreads();
+  if constexpr (W > 1) {
+    if (wave > 0) {
+      Rigid<R> carry = load_rigid(wave_total, 0);
+#pragma unroll
+      for (int w = 1; w < W - 1; ++w)
+        if (w < wave) carry = compose(carry, load_rigid(wave_total, w));
+      excl = compose(carry, excl);
+    }
+  }
+  return excl;
+}
+
+// Exclusive suffix of per-lane force/moment sums (all later lanes of the chain).
+// Contains one __syncthreads().
+template <typename R, int W>
+__device__ __forceinline__ ForceMoment<R> lane_suffix(const ForceMoment<R>& lane_sum, R (&wave_sum)[W][6], int lane,
+                                                      int wave) {
+  const ForceMoment<R> incl = wave_suffix(lane_sum, lane);
+  if (lane == 0) {
+    wave_sum[wave][0] = incl.f.x; wave_sum[wave][1] = incl.f.y; wave_sum[wave][2] = incl.f.z;
+    wave_sum[wave][3] = incl.m.x; wave_sum[wave][4] = incl.m.y; wave_sum[wave][5] = incl.m.z;
+  }
+  ForceMoment<R> excl = wave_shift_down(incl, lane);
+  __syncthreads();
+  if constexpr (W > 1) {
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      if (w > wave) {
+        excl.f = excl.f + V3<R>{wave_sum[w][0], wave_sum[w][1], wave_sum[w][2]};
+        excl.m = excl.m + V3<R>{wave_sum[w][3], wave_sum[w][4], wave_sum[w][5]};
+      }
+    }
+  }
+  return excl;
 }
 
 }  // namespace cufk_amd

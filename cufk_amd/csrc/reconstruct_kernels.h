@@ -1,0 +1,442 @@
+// Reconstruction kernels (reference: src/cufk/csrc/block.cu).
+//
+// One workgroup of W wave64s per chain; lane t owns steps [tK, tK+K) (point s+3 for step s).
+//   reconstruct_forward_kernel     block_forward_kernel (block.cu:157-204)
+//   reconstruct_backward_exact     block_backward_kernel (block.cu:230-313): recomputes the frames
+//   reconstruct_backward_fast      the world-frame force/moment adjoint over the saved positions
+//                                  (the form torsion.cu:204-217 uses), for chains the forward
+//                                  marked regular
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "chain_ops.h"
+#include "staging.h"
+
+namespace cufk_amd {
+
+// When the position-based adjoint is accurate: every bond length positive, every bond angle
+// with sin >= kSinMin, and every coordinate within kScale shortest bonds of the origin (the
+// stored positions then resolve bond directions to about kScale ulp / bond).  float16/bfloat16
+// positions are too coarse, so those chains always take the exact path.
+template <typename T> struct FastPath {
+  static constexpr bool kEnabled = false;
+  static constexpr double kSinMin = 2.0;
+  static constexpr double kScale = 0.0;
+};
+template <> struct FastPath<float> {
+  static constexpr bool kEnabled = true;
+  static constexpr double kSinMin = 0.5;
+  static constexpr double kScale = 256.0;
+};
+template <> struct FastPath<double> {
+  static constexpr bool kEnabled = true;
+  static constexpr double kSinMin = 1.0e-2;
+  static constexpr double kScale = 8192.0;
+};
+
+template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
+  m = fmax(m, fabs(x.x));
+  m = fmax(m, fabs(x.y));
+  return fmax(m, fabs(x.z));
+}
+
+// ============================================================================ forward
+
+// x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v.  When
+// `regular` is non-null, regular[row] receives the fast-path predicate for the chain.
+template <typename T, int W, int K>
+__global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K>;
+  constexpr int kStage = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R stage[kStage];
+  __shared__ R wave_total[W][12];
+  __shared__ R base[12];  // first-frame rotation (row-major) and p2
+  __shared__ R wave_stat[W][3];
+
+  const int steps = points - 3;
+  const int64_t row = blockIdx.x;
+  const T* Lr = lengths + row * (points - 1);
+  const T* Ar = angles + row * (points - 2);
+  const T* Dr = dihedrals + row * (points - 3);
+  T* out = xyz + row * points * 3;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  {
+    R* const dst[3] = {stage, stage + Lay::kStepRow, stage + 2 * Lay::kStepRow};
+    const T* const src[3] = {Lr + 2, Ar + 1, Dr};
+    load_step_rows<Lay, 3>(dst, src, steps, tid);
+  }
+  FirstFrame<R> ff;
+  if (wave == 0) {
+    ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 9; ++i) base[i] = ff.frame[i];
+      base[9] = ff.p2.x;
+      base[10] = ff.p2.y;
+      base[11] = ff.p2.z;
+    }
+  }
+  __syncthreads();
+
+  // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
+  // translation of the lane-local prefix after item i.
+  Rigid<double> q = rigid_identity<double>();
+  R y[K][3];
+  bool ok = true;
+  R lmin = R(1.0e30);
+  const int s0 = tid * K;
+  const int b0 = Lay::lane_step_base(tid);
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (s0 + i < steps) {
+      const R l = stage[b0 + i];
+      const R th = stage[Lay::kStepRow + b0 + i];
+      const R ph = stage[2 * Lay::kStepRow + b0 + i];
+      double s, c, S, C;
+      sin_cos_wide(th, s, c);
+      sin_cos_wide(ph, S, C);
+      step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+      ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
+      lmin = fmin(lmin, l);
+    }
+    y[i][0] = static_cast<R>(q.v[0]);
+    y[i][1] = static_cast<R>(q.v[1]);
+    y[i][2] = static_cast<R>(q.v[2]);
+  }
+
+  // lane_carry's barrier also publishes base[] and retires every read of the step rows,
+  // which the point row below overwrites.
+  const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
+  R F[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) F[i] = base[i];
+  const V3<R> p2 = {base[9], base[10], base[11]};
+
+  // World transform at the lane start: (F, p2) o excl.
+  R gm[9];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) gm[3 * r + c] = F[3 * r] * excl.m[c] + F[3 * r + 1] * excl.m[3 + c] + F[3 * r + 2] * excl.m[6 + c];
+  }
+  const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+
+  R xmax = R(0);
+  const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (s0 + i < steps) {
+      const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+      stage[o0 + 3 * i] = x.x;
+      stage[o0 + 3 * i + 1] = x.y;
+      stage[o0 + 3 * i + 2] = x.z;
+      xmax = abs_max3(xmax, x);
+    }
+  }
+  if (tid == 0) {
+    stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
+    stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
+    stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
+  }
+  if constexpr (FastPath<T>::kEnabled) {
+    if (regular != nullptr) {
+      const bool wave_ok = __all(ok);
+      const R wmin = wave_min(lmin);
+      const R wmax = wave_max(xmax);
+      if (lane == 0) {
+        wave_stat[wave][0] = wave_ok ? R(1) : R(0);
+        wave_stat[wave][1] = wmin;
+        wave_stat[wave][2] = wmax;
+      }
+    }
+  }
+  __syncthreads();
+  if (regular != nullptr && tid == 0) {
+    bool reg = false;
+    if constexpr (FastPath<T>::kEnabled) {
+      reg = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= FastPath<T>::kSinMin;
+      R m = fmin(ff.L0, ff.L1);
+      R x = abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2);
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        reg = reg && wave_stat[w][0] != R(0);
+        m = fmin(m, wave_stat[w][1]);
+        x = fmax(x, wave_stat[w][2]);
+      }
+      reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * m;
+    }
+    regular[row] = reg ? 1 : 0;
+  }
+  store_point_row<Lay>(out, stage, points, tid);
+}
+
+// ============================================================================ exact backward
+
+// World-frame adjoint with exact frame axes, recomputing the forward scan from the
+// parameters (valid for every finite input):
+//   F_i = sum_{j>=i} g_j,  M_i = sum_{j>=i} x_j x g_j,  tau = M_{k+3} - x_{k+2} x F_{k+3}
+//   dL/dL[k+2] = R_k[:,0].F_{k+3},  dL/dA[k+1] = -R_k[:,2].tau,  dL/dD[k] = R_{k-1}[:,0].tau
+// with R_k the world rotation after step k; first-frame terms restate block.cu:206-228.
+// Positions are relative to x2 (the moments are translation invariant).  Grid-stride over
+// chains; chains with skip[row] != 0 are left to the fast kernel.
+template <typename T, int W, int K>
+__global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
+    T* __restrict__ grad_dihedrals, const uint8_t* __restrict__ skip, int points, int batch) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K>;
+  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];  // parameters
+  __shared__ __align__(16) R gstage[Lay::kPointRow];     // upstream gradient, then the outputs
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
+
+  const int steps = points - 3;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int s0 = tid * K;
+  const int b0 = Lay::lane_step_base(tid);
+  const int o0 = Lay::lane_point_base(tid);
+
+  for (int64_t row = blockIdx.x; row < batch; row += gridDim.x) {
+    if (skip != nullptr && skip[row] != 0) continue;  // uniform across the workgroup
+    const T* Lr = lengths + row * (points - 1);
+    const T* Ar = angles + row * (points - 2);
+    const T* Dr = dihedrals + row * (points - 3);
+    const T* Gr = grad_xyz + row * points * 3;
+    T* gLr = grad_lengths + row * (points - 1);
+    T* gAr = grad_angles + row * (points - 2);
+    T* gDr = grad_dihedrals + row * (points - 3);
+
+    {
+      R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
+      const T* const src[3] = {Lr + 2, Ar + 1, Dr};
+      load_step_rows<Lay, 3>(dst, src, steps, tid);
+      R* const gdst[1] = {gstage};
+      const T* const gsrc[1] = {Gr};
+      load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
+    }
+    const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+    __syncthreads();
+
+    // Pass 1: lane-local scan (double); keep sin/cos; Y = sum_i y_i g_i^T and sum_i g_i.
+    Rigid<double> qd = rigid_identity<double>();
+    R sc[K][4];
+    R Y[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) Y[i] = R(0);
+    V3<R> gsum = {R(0), R(0), R(0)};
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      sc[i][0] = sc[i][1] = sc[i][2] = sc[i][3] = R(0);
+      if (s0 + i < steps) {
+        const R l = pstage[b0 + i];
+        double s, c, S, C;
+        sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
+        sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+        sc[i][0] = static_cast<R>(s);
+        sc[i][1] = static_cast<R>(c);
+        sc[i][2] = static_cast<R>(S);
+        sc[i][3] = static_cast<R>(C);
+        step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
+        const V3<R> g = load3(&gstage[o0 + 3 * i]);
+        const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+          Y[3 * a + 0] += yv[a] * g.x;
+          Y[3 * a + 1] += yv[a] * g.y;
+          Y[3 * a + 2] += yv[a] * g.z;
+        }
+        gsum = gsum + g;
+      }
+    }
+
+    const Rigid<R> q = narrow_rigid<R>(qd);
+    const Rigid<R> excl = lane_carry<R, W>(q, wave_total, lane, wave);
+
+    // World frame at the lane start, origin at x2: R0 = F excl.m, X0 = F excl.v.
+    R R0[9];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+        R0[3 * r + c] = ff.frame[3 * r] * excl.m[c] + ff.frame[3 * r + 1] * excl.m[3 + c] + ff.frame[3 * r + 2] * excl.m[6 + c];
+    }
+    const V3<R> X0 = rot_apply(ff.frame, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+
+    // Lane moment sum_i (X0 + R0 y_i) x g_i = X0 x gsum + axial part of R0 Y.
+    R Z[9];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) Z[3 * r + c] = R0[3 * r] * Y[c] + R0[3 * r + 1] * Y[3 + c] + R0[3 * r + 2] * Y[6 + c];
+    }
+    ForceMoment<R> lane_sum;
+    lane_sum.f = gsum;
+    lane_sum.m = cross(X0, gsum) + V3<R>{Z[5] - Z[7], Z[6] - Z[2], Z[1] - Z[3]};
+
+    // World state after the lane's last step.
+    R Rm[9];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) Rm[3 * r + c] = R0[3 * r] * q.m[c] + R0[3 * r + 1] * q.m[3 + c] + R0[3 * r + 2] * q.m[6 + c];
+    }
+    V3<R> x = X0 + rot_apply(R0, V3<R>{q.v[0], q.v[1], q.v[2]});
+
+    const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
+
+    // Pass 2: walk the lane's steps backwards; the outputs of step s replace g_{s+3} in LDS.
+    V3<R> Fs = tail.f, Ms = tail.m;
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {
+      if (s0 + i < steps) {
+        const V3<R> g = load3(&gstage[o0 + 3 * i]);
+        Fs = Fs + g;
+        Ms = Ms + cross(x, g);
+        const R l = pstage[b0 + i];
+        const V3<R> col0 = {Rm[0], Rm[3], Rm[6]};
+        const V3<R> col2 = {Rm[2], Rm[5], Rm[8]};
+        const V3<R> xp = x - l * col0;
+        const V3<R> tau = Ms - cross(xp, Fs);
+        const R gl = dot(col0, Fs);
+        const R ga = -dot(col2, tau);
+        step_backward(Rm, sc[i][0], sc[i][1], sc[i][2], sc[i][3]);
+        const R gd = dot(V3<R>{Rm[0], Rm[3], Rm[6]}, tau);
+        gstage[o0 + 3 * i] = gl;
+        gstage[o0 + 3 * i + 1] = ga;
+        gstage[o0 + 3 * i + 2] = gd;
+        x = xp;
+      }
+    }
+    if (tid == 0) {
+      // First-frame parameters (block.cu:206-228); x2 is the origin, so M_2 = M_3.
+      const V3<R> g1 = load3(&gstage[3]);
+      const V3<R> g2 = load3(&gstage[6]);
+      const V3<R> F2 = Fs + g2;
+      const V3<R> x1 = ff.p1 - ff.p2;
+      const V3<R> tau2 = Ms - cross(x1, F2);
+      gLr[0] = narrow<T>(dot(ff.d0, F2 + g1));
+      gLr[1] = narrow<T>(dot(ff.d1, F2));
+      gAr[0] = narrow<T>(-dot(cross(ff.d0, ff.t0), tau2));
+    }
+    __syncthreads();
+    store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gstage, steps, tid);
+    __syncthreads();  // the next chain's loads overwrite the staging rows
+  }
+}
+
+// ============================================================================ fast backward
+
+// Position-based adjoint for chains with regular[row] != 0 (A.6 of the design notes):
+//   T_j = M_j - x_{j-1} x F_j,  dL/dL[j-1] = u(b_{j-1}).F_j,
+//   dL/dA[j-2] = u(b_{j-1} x b_{j-2}).T_j,  dL/dD[j-3] = u(b_{j-2}).T_j,  b_i = x_{i+1} - x_i,
+// where F_j, M_j are suffix sums of g and x x g.  Positions are taken relative to x2.
+template <typename T, int W, int K>
+__global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
+    const T* __restrict__ xyz, const T* __restrict__ grad_xyz, const uint8_t* __restrict__ regular,
+    T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K>;
+  __shared__ __align__(16) R xs[Lay::kPointRow];
+  __shared__ __align__(16) R gs[Lay::kPointRow];  // upstream gradient, then the outputs
+  __shared__ R wave_sum[W][6];
+
+  const int64_t row = blockIdx.x;
+  if (regular[row] == 0) return;  // the exact kernel handles this chain
+  const int steps = points - 3;
+  const T* Xr = xyz + row * points * 3;
+  const T* Gr = grad_xyz + row * points * 3;
+  T* gLr = grad_lengths + row * (points - 1);
+  T* gAr = grad_angles + row * (points - 2);
+  T* gDr = grad_dihedrals + row * (points - 3);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  {
+    R* const dst[2] = {xs, gs};
+    const T* const src[2] = {Xr, Gr};
+    load_point_rows<Lay, 2>(dst, src, points, tid);
+  }
+  __syncthreads();
+
+  const V3<R> c = load3(&xs[6]);
+  auto pos = [&](int p) { return load3(&xs[Lay::point_slot(3 * p)]) - c; };
+  const int s0 = tid * K;
+  const int o0 = Lay::lane_point_base(tid);
+  const int last = (steps - s0 < K ? steps - s0 : K) - 1;  // last valid item of this lane
+
+  ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (i <= last) {
+      const V3<R> x = load3(&xs[o0 + 3 * i]) - c;
+      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      lane_sum.f = lane_sum.f + g;
+      lane_sum.m = lane_sum.m + cross(x, g);
+    }
+  }
+  const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
+
+  V3<R> F = tail.f, M = tail.m;
+  V3<R> xa, xb, xc, u1, b1;  // x_p, x_{p-1}, x_{p-2}; unit and raw bond p-1 -> p
+  if (last >= 0) {
+    const int p = 3 + s0 + last;
+    xa = pos(p);
+    xb = pos(p - 1);
+    xc = pos(p - 2);
+    b1 = xa - xb;
+    u1 = rsqrt_r(dot(b1, b1)) * b1;
+  }
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    if (i <= last) {
+      const int p = 3 + s0 + i;
+      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      F = F + g;
+      M = M + cross(xa, g);
+      const V3<R> Tq = M - cross(xb, F);
+      const V3<R> b2 = xb - xc;
+      const V3<R> u2 = rsqrt_r(dot(b2, b2)) * b2;
+      const V3<R> n = cross(b1, b2);
+      gs[o0 + 3 * i] = dot(u1, F);
+      gs[o0 + 3 * i + 1] = dot(n, Tq) * rsqrt_r(dot(n, n));
+      gs[o0 + 3 * i + 2] = dot(u2, Tq);
+      xa = xb;
+      xb = xc;
+      xc = pos(p - 3);
+      b1 = b2;
+      u1 = u2;
+    }
+  }
+  if (tid == 0) {
+    // Atoms 2 and 1: dL/dL[1], dL/dA[0] and dL/dL[0].  Here xa = x2 (the origin), xb = x1, xc = x0.
+    const V3<R> g2 = load3(&gs[6]);
+    const V3<R> g1 = load3(&gs[3]);
+    F = F + g2;
+    const V3<R> Tq = M - cross(xb, F);
+    const V3<R> b2 = xb - xc;
+    const V3<R> n = cross(b1, b2);
+    gLr[1] = narrow<T>(dot(u1, F));
+    gAr[0] = narrow<T>(dot(n, Tq) * rsqrt_r(dot(n, n)));
+    gLr[0] = narrow<T>(dot(rsqrt_r(dot(b2, b2)) * b2, F + g1));
+  }
+  __syncthreads();
+  store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gs, steps, tid);
+}
+
+}  // namespace cufk_amd

@@ -1,0 +1,226 @@
+// LDS staging of chain rows.
+//
+// Global rows are streamed with 16-byte vector accesses (coalesced across the workgroup) into
+// LDS layouts in which every lane's K steps (or K points) are contiguous and 16-byte aligned,
+// padded by 4 words per lane:
+//   step layout:  step s        -> slot s + 4*(s/K)              (lane stride K+4 words)
+//   point layout: flat xyz e>=9 -> slot 12 + e' + 4*(e'/(3K))    (e' = e-9, lane stride 3K+4)
+//                 e < 9 (points 0..2) -> slot e
+// Lane t owns steps [tK, tK+K) and points [3+tK, 3+tK+K).  With K a multiple of 4 the lane
+// strides are 4 mod 32 words, so the lanes' ds_read_b128 / ds_write_b128 hit disjoint banks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "chain_ops.h"
+
+namespace cufk_amd {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef double f64x2u __attribute__((ext_vector_type(2), aligned(8)));
+
+template <int W, int K> struct Layout {
+  static_assert(K % 4 == 0, "lane segments must be whole 16-byte groups");
+  static constexpr int kWaves = W;
+  static constexpr int kItems = K;
+  static constexpr int kLanes = 64 * W;
+  static constexpr int kCap = kLanes * K;  // steps per chain
+  static constexpr int kStepStride = K + 4;
+  static constexpr int kStepRow = kLanes * kStepStride;
+  static constexpr int kPointStride = 3 * K + 4;
+  static constexpr int kPointRow = 12 + kLanes * kPointStride;
+  __device__ __forceinline__ static int step_slot(int s) { return s + 4 * (s / K); }
+  __device__ __forceinline__ static int point_slot(int e) {
+    if (e < 9) return e;
+    const int t = e - 9;
+    return 12 + t + 4 * (t / (3 * K));
+  }
+  __device__ __forceinline__ static int lane_step_base(int tid) { return tid * kStepStride; }
+  __device__ __forceinline__ static int lane_point_base(int tid) { return 12 + tid * kPointStride; }
+};
+
+// 16-byte global access unit for T: 4 floats or 2 doubles (dword-aligned rows suffice);
+// float16/bfloat16 rows are only 2-byte aligned and move one element at a time.
+template <typename T> struct Unit {
+  static constexpr int kElems = 1;
+};
+template <> struct Unit<float> {
+  static constexpr int kElems = 4;
+  typedef f32x4u Global;
+  typedef f32x4 Local;
+};
+template <> struct Unit<double> {
+  static constexpr int kElems = 2;
+  typedef f64x2u Global;
+  typedef f64x2 Local;
+};
+
+// Rows of NR arrays into LDS: dst[r][slot(first + e)] = src[r][first + e] for e in [0, n).
+// Two-phase: every global load of the thread is issued into registers before the first LDS
+// write, so a workgroup pays one memory latency per staging phase, not one per group.
+// MaxN bounds n at compile time.
+template <int NR, int MaxN, int Lanes, typename T, typename SlotFn>
+__device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
+                                           int tid, SlotFn slot) {
+  using R = compute_t<T>;
+  if constexpr (Unit<T>::kElems > 1) {
+    constexpr int E = Unit<T>::kElems;
+    constexpr int kPer = (MaxN / E + Lanes - 1) / Lanes;
+    typename Unit<T>::Local buf[NR][kPer];
+    R tail[NR];
+    const int groups = n / E;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lanes;
+      if (g < groups) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) buf[r][j] = *reinterpret_cast<const typename Unit<T>::Global*>(src[r] + first + E * g);
+      }
+    }
+    const int te = E * groups + tid;  // at most E-1 tail elements, one per low thread
+    if (te < n) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) tail[r] = src[r][first + te];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lanes;
+      if (g < groups) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) *reinterpret_cast<typename Unit<T>::Local*>(dst[r] + slot(first + E * g)) = buf[r][j];
+      }
+    }
+    if (te < n) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) dst[r][slot(first + te)] = tail[r];
+    }
+  } else {
+    constexpr int kPer = (MaxN + Lanes - 1) / Lanes;
+    R buf[NR][kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + j * Lanes;
+      if (e < n) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) buf[r][j] = widen(src[r][first + e]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + j * Lanes;
+      if (e < n) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) dst[r][slot(first + e)] = buf[r][j];
+      }
+    }
+  }
+}
+
+// NR step rows (n <= kCap elements each) into step layouts.
+template <typename Lay, int NR, typename T>
+__device__ __forceinline__ void load_step_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int n, int tid) {
+  stage_rows<NR, Lay::kCap, Lay::kLanes, T>(dst, src, 0, n, tid, [](int s) { return Lay::step_slot(s); });
+}
+
+// NR (points, 3) rows into point layouts.
+template <typename Lay, int NR, typename T>
+__device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int points,
+                                                int tid) {
+  if (tid < 9) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) dst[r][tid] = widen(src[r][tid]);
+  }
+  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, T>(dst, src, 9, 3 * points - 9, tid,
+                                                [](int e) { return Lay::point_slot(e); });
+}
+
+// dst[s] = src[step_slot(s)] for s in [0, n).
+template <typename Lay, typename T>
+__device__ __forceinline__ void store_step_row(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int n, int tid) {
+  if constexpr (std::is_same_v<T, float>) {
+    const int groups = n >> 2;
+    for (int g = tid; g < groups; g += Lay::kLanes)
+      *reinterpret_cast<f32x4u*>(dst + 4 * g) = *reinterpret_cast<const f32x4*>(src + Lay::step_slot(4 * g));
+    for (int s = 4 * groups + tid; s < n; s += Lay::kLanes) dst[s] = src[Lay::step_slot(s)];
+  } else if constexpr (std::is_same_v<T, double>) {
+    const int groups = n >> 1;
+    for (int g = tid; g < groups; g += Lay::kLanes)
+      *reinterpret_cast<f64x2u*>(dst + 2 * g) = *reinterpret_cast<const f64x2*>(src + Lay::step_slot(2 * g));
+    if ((n & 1) && tid == 0) dst[n - 1] = src[Lay::step_slot(n - 1)];
+  } else {
+    for (int s = tid; s < n; s += Lay::kLanes) dst[s] = narrow<T>(src[Lay::step_slot(s)]);
+  }
+}
+
+// dst[e] = src[point_slot(e)] for e in [0, 3*points).
+template <typename Lay, typename T>
+__device__ __forceinline__ void store_point_row(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int points,
+                                                int tid) {
+  const int n = 3 * points - 9;
+  if (tid < 9) dst[tid] = narrow<T>(src[tid]);
+  if constexpr (std::is_same_v<T, float>) {
+    const int groups = n >> 2;
+    for (int g = tid; g < groups; g += Lay::kLanes)
+      *reinterpret_cast<f32x4u*>(dst + 9 + 4 * g) = *reinterpret_cast<const f32x4*>(src + Lay::point_slot(9 + 4 * g));
+    for (int e = 4 * groups + tid; e < n; e += Lay::kLanes) dst[9 + e] = src[Lay::point_slot(9 + e)];
+  } else if constexpr (std::is_same_v<T, double>) {
+    const int groups = n >> 1;
+    for (int g = tid; g < groups; g += Lay::kLanes)
+      *reinterpret_cast<f64x2u*>(dst + 9 + 2 * g) = *reinterpret_cast<const f64x2*>(src + Lay::point_slot(9 + 2 * g));
+    if ((n & 1) && tid == 0) dst[9 + n - 1] = src[Lay::point_slot(9 + n - 1)];
+  } else {
+    for (int e = tid; e < n; e += Lay::kLanes) dst[9 + e] = narrow<T>(src[Lay::point_slot(9 + e)]);
+  }
+}
+
+// Three step-indexed gradient rows written interleaved into the point layout: the outputs of
+// step s (lane t, item i) occupy slots lane_point_base(t) + 3i + {0,1,2}, i.e. exactly the
+// upstream-gradient slots of point s+3, which the owning lane has consumed by then.
+//   a[s + offset_a] for s in [0, steps), likewise b and c.
+template <typename Lay, typename T>
+__device__ __forceinline__ void store_interleaved_rows(T* __restrict__ a, T* __restrict__ b, T* __restrict__ c,
+                                                       const compute_t<T>* __restrict__ src, int steps, int tid) {
+  if constexpr (std::is_same_v<T, float>) {
+    const int groups = steps >> 2;  // 4 steps never straddle a lane (K % 4 == 0)
+    for (int g = tid; g < groups; g += Lay::kLanes) {
+      const float* p = src + Lay::point_slot(9 + 12 * g);
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(p);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(p + 4);
+      const f32x4 v2 = *reinterpret_cast<const f32x4*>(p + 8);
+      *reinterpret_cast<f32x4u*>(a + 4 * g) = f32x4{v0.x, v0.w, v1.z, v2.y};
+      *reinterpret_cast<f32x4u*>(b + 4 * g) = f32x4{v0.y, v1.x, v1.w, v2.z};
+      *reinterpret_cast<f32x4u*>(c + 4 * g) = f32x4{v0.z, v1.y, v2.x, v2.w};
+    }
+    for (int s = 4 * groups + tid; s < steps; s += Lay::kLanes) {
+      const float* p = src + Lay::point_slot(9 + 3 * s);
+      a[s] = p[0];
+      b[s] = p[1];
+      c[s] = p[2];
+    }
+  } else {
+    for (int s = tid; s < steps; s += Lay::kLanes) {
+      const compute_t<T>* p = src + Lay::point_slot(9 + 3 * s);
+      a[s] = narrow<T>(p[0]);
+      b[s] = narrow<T>(p[1]);
+      c[s] = narrow<T>(p[2]);
+    }
+  }
+}
+
+// Same for two interleaved rows written as (x0, y0, -, x1, y1, -, ...) into point slots,
+// stored to a[2s], a[2s+1] (torsion raw-pair gradients).
+template <typename Lay, typename T>
+__device__ __forceinline__ void store_interleaved_pairs(T* __restrict__ out, const compute_t<T>* __restrict__ src,
+                                                        int steps, int tid) {
+  for (int s = tid; s < steps; s += Lay::kLanes) {
+    const compute_t<T>* p = src + Lay::point_slot(9 + 3 * s);
+    out[2 * s] = narrow<T>(p[0]);
+    out[2 * s + 1] = narrow<T>(p[1]);
+  }
+}
+
+}  // namespace cufk_amd

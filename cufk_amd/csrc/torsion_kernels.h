@@ -1,0 +1,255 @@
+// Torsion-only kernels (reference: src/cufk/csrc/torsion.cu).
+//
+// Step k uses bond length l[(k+2)%3], bond angle (k+1)%3 and the normalised raw pair k
+// (torsion.cu:67-73, 119-141).  K is a multiple of 12: lane segments are whole 16-byte groups
+// and every lane's item i has phase i % 3.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "chain_ops.h"
+#include "staging.h"
+
+namespace cufk_amd {
+
+struct TorsionArgs {
+  float length[3];
+  double sin[3];
+  double cos[3];
+  float inv_length[3];  // 1.0f / length, formed in float (torsion.cu:216)
+};
+
+// Raw pairs (sin, cos interleaved, src[2s], src[2s+1]) into two step-layout rows, two-phase
+// like stage_rows: all global loads of the thread are issued before the LDS writes.
+template <typename Lay, typename T>
+__device__ __forceinline__ void load_pair_rows(compute_t<T>* __restrict__ srow, compute_t<T>* __restrict__ crow,
+                                               const T* __restrict__ src, int steps, int tid) {
+  using R = compute_t<T>;
+  if constexpr (std::is_same_v<T, float>) {
+    constexpr int kPer = (Lay::kCap / 2 + Lay::kLanes - 1) / Lay::kLanes;
+    const int groups = steps >> 1;  // two pairs per 16 bytes; steps 2g, 2g+1 share a lane (K even)
+    f32x4 buf[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lay::kLanes;
+      if (g < groups) buf[j] = *reinterpret_cast<const f32x4u*>(src + 4 * g);
+    }
+    float ts = 0.0f, tc = 0.0f;
+    const bool tail = (steps & 1) && tid == 0;
+    if (tail) {
+      ts = src[2 * (steps - 1)];
+      tc = src[2 * (steps - 1) + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lay::kLanes;
+      if (g < groups) {
+        const int slot = Lay::step_slot(2 * g);
+        srow[slot] = buf[j].x;
+        crow[slot] = buf[j].y;
+        srow[slot + 1] = buf[j].z;
+        crow[slot + 1] = buf[j].w;
+      }
+    }
+    if (tail) {
+      srow[Lay::step_slot(steps - 1)] = ts;
+      crow[Lay::step_slot(steps - 1)] = tc;
+    }
+  } else {
+    constexpr int kPer = (Lay::kCap + Lay::kLanes - 1) / Lay::kLanes;
+    R bs[kPer], bc[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int s = tid + j * Lay::kLanes;
+      if (s < steps) {
+        bs[j] = widen(src[2 * s]);
+        bc[j] = widen(src[2 * s + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int s = tid + j * Lay::kLanes;
+      if (s < steps) {
+        srow[Lay::step_slot(s)] = bs[j];
+        crow[Lay::step_slot(s)] = bc[j];
+      }
+    }
+  }
+}
+
+// Forward (torsion.cu:254-295).
+template <typename T, int W, int K>
+__global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __restrict__ raw_pairs, int64_t raw_stride,
+                                                                 TorsionArgs cst, T* __restrict__ xyz, int points) {
+  static_assert(K % 12 == 0, "torsion plans keep phases lane-invariant and segments 16-byte aligned");
+  using R = compute_t<T>;
+  using Lay = Layout<W, K>;
+  constexpr int kStage = 2 * Lay::kStepRow > Lay::kPointRow ? 2 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R stage[kStage];
+  __shared__ R wave_total[W][12];
+
+  const int steps = points - 3;
+  const int64_t row = blockIdx.x;
+  const T* raw = raw_pairs + row * raw_stride;
+  T* out = xyz + row * points * 3;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  load_pair_rows<Lay>(stage, stage + Lay::kStepRow, raw, steps, tid);
+  __syncthreads();
+
+  // Serial part in double with the float64 bond-angle sin/cos (the reference rounds them to
+  // the compute type, torsion.cu:226-227, which biases |M| per phase along the chain).
+  Rigid<double> q = rigid_identity<double>();
+  R y[K][3];
+  const int s0 = tid * K;
+  const int b0 = Lay::lane_step_base(tid);
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (s0 + i < steps) {
+      const int lp = (i + 2) % 3;  // torsion.cu:67-69
+      const int ap = (i + 1) % 3;  // torsion.cu:71-73
+      double S, C;
+      pair_unit(stage[b0 + i], stage[Lay::kStepRow + b0 + i], S, C);
+      step_forward(q.m, q.v, static_cast<double>(cst.length[lp]), cst.sin[ap], cst.cos[ap], S, C);
+    }
+    y[i][0] = static_cast<R>(q.v[0]);
+    y[i][1] = static_cast<R>(q.v[1]);
+    y[i][2] = static_cast<R>(q.v[2]);
+  }
+
+  const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
+
+  // Constant base (torsion.cu:149-166): x0 = 0, x1 = (l0,0,0), x2 = (l0 - l1 c0, l1 s0, 0),
+  // F = [(-c0, s0, 0) | (-s0, -c0, 0) | (0, 0, 1)].
+  const R s0a = static_cast<R>(cst.sin[0]), c0a = static_cast<R>(cst.cos[0]);
+  const R l0 = static_cast<R>(cst.length[0]), l1 = static_cast<R>(cst.length[1]);
+  const V3<R> p2 = {l0 - l1 * c0a, l1 * s0a, R(0)};
+  R gm[9];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    gm[c] = -c0a * excl.m[c] - s0a * excl.m[3 + c];
+    gm[3 + c] = s0a * excl.m[c] - c0a * excl.m[3 + c];
+    gm[6 + c] = excl.m[6 + c];
+  }
+  const V3<R> gv = {p2.x + (-c0a * excl.v[0] - s0a * excl.v[1]), p2.y + (s0a * excl.v[0] - c0a * excl.v[1]),
+                    p2.z + excl.v[2]};
+
+  const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (s0 + i < steps) {
+      const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+      stage[o0 + 3 * i] = x.x;
+      stage[o0 + 3 * i + 1] = x.y;
+      stage[o0 + 3 * i + 2] = x.z;
+    }
+  }
+  if (tid == 0) {
+    stage[0] = R(0); stage[1] = R(0); stage[2] = R(0);
+    stage[3] = l0;   stage[4] = R(0); stage[5] = R(0);
+    stage[6] = p2.x; stage[7] = p2.y; stage[8] = p2.z;
+  }
+  __syncthreads();
+  store_point_row<Lay>(out, stage, points, tid);
+}
+
+// Backward (torsion.cu:297-381) over the saved positions:
+//   dphi_k = (1/l_{(k+1)%3}) (x_{k+2} - x_{k+1}) . (M_{k+3} - x_{k+2} x F_{k+3}),
+//   raw grad = dphi (rc, -rs) / max(rs^2 + rc^2, 1e-16) (torsion.cu:173-182),
+// with positions relative to x2 (the moments are translation invariant).
+template <typename T, int W, int K>
+__global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __restrict__ raw_pairs, int64_t raw_stride,
+                                                                  const T* __restrict__ xyz, const T* __restrict__ grad_xyz,
+                                                                  T* __restrict__ grad_raw, int64_t grad_raw_stride,
+                                                                  TorsionArgs cst, int points) {
+  static_assert(K % 12 == 0, "torsion plans keep phases lane-invariant and segments 16-byte aligned");
+  using R = compute_t<T>;
+  using Lay = Layout<W, K>;
+  __shared__ __align__(16) R xs[Lay::kPointRow];
+  __shared__ __align__(16) R gs[Lay::kPointRow];  // upstream gradient, then the raw-pair gradients
+  // float64 rows would overflow LDS at the largest plan; those read raw pairs from global.
+  constexpr bool kStageRaw = sizeof(R) == 4;
+  __shared__ __align__(16) R rstage[kStageRaw ? 2 * Lay::kStepRow : 4];
+  __shared__ R wave_sum[W][6];
+
+  const int steps = points - 3;
+  const int64_t row = blockIdx.x;
+  const T* raw = raw_pairs + row * raw_stride;
+  const T* Xr = xyz + row * points * 3;
+  const T* Gr = grad_xyz + row * points * 3;
+  T* graw = grad_raw + row * grad_raw_stride;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  if constexpr (kStageRaw) load_pair_rows<Lay>(rstage, rstage + Lay::kStepRow, raw, steps, tid);
+  {
+    R* const dst[2] = {xs, gs};
+    const T* const src[2] = {Xr, Gr};
+    load_point_rows<Lay, 2>(dst, src, points, tid);
+  }
+  __syncthreads();
+
+  const V3<R> c = load3(&xs[6]);
+  auto pos = [&](int p) { return load3(&xs[Lay::point_slot(3 * p)]) - c; };
+  const int s0 = tid * K;
+  const int o0 = Lay::lane_point_base(tid);
+  const int b0 = Lay::lane_step_base(tid);
+  const int last = (steps - s0 < K ? steps - s0 : K) - 1;
+
+  ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (i <= last) {
+      const V3<R> x = load3(&xs[o0 + 3 * i]) - c;
+      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      lane_sum.f = lane_sum.f + g;
+      lane_sum.m = lane_sum.m + cross(x, g);
+    }
+  }
+  const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
+
+  V3<R> F = tail.f, M = tail.m;
+  V3<R> xa, xb, xc;  // x_p, x_{p-1}, x_{p-2}
+  if (last >= 0) {
+    const int p = 3 + s0 + last;
+    xa = pos(p);
+    xb = pos(p - 1);
+    xc = pos(p - 2);
+  }
+  const R eps2 = static_cast<R>(1.0e-8f * 1.0e-8f);
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    if (i <= last) {
+      const int p = 3 + s0 + i;
+      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      F = F + g;
+      M = M + cross(xa, g);
+      const R dphi = static_cast<R>(cst.inv_length[(i + 1) % 3]) * dot(xb - xc, M - cross(xb, F));
+      R rs, rc;
+      if constexpr (kStageRaw) {
+        rs = rstage[b0 + i];
+        rc = rstage[Lay::kStepRow + b0 + i];
+      } else {
+        rs = widen(raw[2 * (p - 3)]);
+        rc = widen(raw[2 * (p - 3) + 1]);
+      }
+      const R n2 = rs * rs + rc * rc;
+      const R scale = dphi / (n2 < eps2 ? eps2 : n2);
+      gs[o0 + 3 * i] = rc * scale;
+      gs[o0 + 3 * i + 1] = -rs * scale;
+      xa = xb;
+      xb = xc;
+      xc = pos(p - 3);
+    }
+  }
+  __syncthreads();
+  store_interleaved_pairs<Lay>(graw, gs, steps, tid);
+}
+
+}  // namespace cufk_amd

@@ -68,6 +68,18 @@ int cufk_reconstruct_fwd(int dtype, const void* lengths, const void* angles, con
                          void* xyz, int64_t batch, int64_t points, void* stream);
 
 /*
+ * Forward reconstruction that also classifies each chain for the position-based backward:
+ * chain_regular[b] = 1 when every bond length is positive, every bond angle has sin >= 0.5
+ * (float32; 1e-2 for float64) and every coordinate lies within 256 (float32; 8192 for float64)
+ * shortest bonds of the origin; 0 otherwise and always 0 for float16/bfloat16.  Same inputs and
+ * output as cufk_reconstruct_fwd; chain_regular is a (B,) byte array.  No reference counterpart:
+ * the reference's forward (block.cu:319-329) saves only the inputs.
+ */
+int cufk_reconstruct_fwd_flagged(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                 const void* p0, const void* first_direction, const void* initial_normal, void* xyz,
+                                 uint8_t* chain_regular, int64_t batch, int64_t points, void* stream);
+
+/*
  * Backward reconstruction: dL/d(lengths, angles, dihedrals) from grad_xyz (B, N, 3).
  * Replaces block.cu:331-365 (backward_cuda_impl) and block_backward_kernel
  * (block.cu:230-313).  The anchors receive no gradient (block.cu:427).
@@ -76,6 +88,18 @@ int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, con
                          const void* p0, const void* first_direction, const void* initial_normal,
                          const void* grad_xyz, void* grad_lengths, void* grad_angles, void* grad_dihedrals,
                          int64_t batch, int64_t points, void* stream);
+
+/*
+ * Backward reconstruction given the forward's own output: chains with chain_regular[b] != 0
+ * take the position-based adjoint over xyz (the force/moment form the reference's torsion
+ * backward uses, torsion.cu:204-217), the others the exact recompute of cufk_reconstruct_bwd.
+ * xyz and chain_regular must be exactly what cufk_reconstruct_fwd_flagged wrote for these
+ * inputs.  Replaces block.cu:331-365 for callers that keep the forward output.
+ */
+int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                               const void* p0, const void* first_direction, const void* initial_normal,
+                               const void* xyz, const uint8_t* chain_regular, const void* grad_xyz, void* grad_lengths,
+                               void* grad_angles, void* grad_dihedrals, int64_t batch, int64_t points, void* stream);
 
 /*
  * Torsion-only forward from raw interleaved (sin, cos) pairs, raw row b at

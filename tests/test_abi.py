@@ -23,6 +23,8 @@ def lib():
     i64, vp = ctypes.c_int64, ctypes.c_void_p
     lib.cufk_reconstruct_fwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_reconstruct_bwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_fwd_flagged.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
     lib.cufk_error_string.restype = ctypes.c_char_p
@@ -40,7 +42,9 @@ def test_header_declares_the_entry_points():
         "cufk_error_string",
         "cufk_max_steps",
         "cufk_reconstruct_bwd",
+        "cufk_reconstruct_bwd_saved",
         "cufk_reconstruct_fwd",
+        "cufk_reconstruct_fwd_flagged",
         "cufk_torsion_bwd",
         "cufk_torsion_fwd",
         "cufk_version",
@@ -83,6 +87,14 @@ def test_reconstruct_status_paths(lib):
     assert b(0, p, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
     assert b(0, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL
     assert b(0, p, p, p, p, p, p, p, p, p, p, 0, 10, null) == OK
+    ff = lib.cufk_reconstruct_fwd_flagged
+    assert ff(9, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert ff(0, p, p, p, p, p, p, p, null, 0, 10, null) == OK
+    assert ff(0, p, p, p, p, p, p, null, p, 4, 10, null) == ERR_NULL
+    bs = lib.cufk_reconstruct_bwd_saved
+    assert bs(0, p, p, p, p, p, p, p, null, p, p, p, p, 4, 10, null) == ERR_NULL  # flags are required
+    assert bs(0, p, p, p, p, p, p, p, p, p, p, p, p, 4, 3, null) == ERR_POINTS
+    assert bs(0, p, p, p, p, p, p, p, p, p, p, p, p, 0, 10, null) == OK
 
 
 def test_torsion_status_paths(lib):

@@ -320,3 +320,119 @@ def test_full_size_config2_sampled(cufk, device):
     ref_g = o.reconstruct_backward(sub["lengths"], sub["angles"], sub["dihedrals"], sub["grad"], **_anchor_np(sub))
     for got, want in zip(grads, ref_g):
         assert np.abs(got[idx].double().cpu().numpy() - want).max() <= 2e-4 * np.abs(want).max()
+
+
+# ----------------------------------------------------------------- the two backward paths
+
+
+def _abi():
+    import ctypes
+
+    import cufk_amd
+
+    lib = ctypes.CDLL(str(cufk_amd._native.HIP_LIBRARY))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.cufk_reconstruct_fwd_flagged.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_bwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    return lib
+
+
+_CODES = {torch.float32: 0, torch.float64: 1, torch.float16: 2, torch.bfloat16: 3}
+
+
+def _flagged_forward(lib, L, A, D, an):
+    B, N = L.shape[0], L.shape[1] + 1
+    xyz = torch.empty(B, N, 3, device=L.device, dtype=L.dtype)
+    reg = torch.full((B,), 7, device=L.device, dtype=torch.uint8)
+    p = lambda t: t.data_ptr()  # noqa: E731
+    rc = lib.cufk_reconstruct_fwd_flagged(_CODES[L.dtype], p(L), p(A), p(D), p(an[0]), p(an[1]), p(an[2]), p(xyz), p(reg),
+                                          B, N, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    return xyz, reg
+
+
+def _anchors3(d, dtype, device):
+    if "p0" in d:
+        return tuple(_dev(d[k], dtype, device) for k in ("p0", "first_direction", "initial_normal"))
+    return (_dev([0.0, 0, 0], dtype, device), _dev([1.0, 0, 0], dtype, device), _dev([0.0, 0, 1], dtype, device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.bfloat16])
+def test_regularity_flags(cufk, device, dtype):
+    lib = _abi()
+    d = _inputs(6, 300, seed=21, anchors=True, dtype=dtype)
+    d["lengths"][1, 7] = -d["lengths"][1, 7]  # negative bond
+    small = 0.2 if dtype != torch.float64 else 0.005  # below the fast-path sine threshold
+    d["angles"][2, 40] = small
+    d["angles"][3, 0] = math.pi - small  # first-frame angle
+    d["lengths"][4, 1] = 0.0  # zero bond
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    xyz, reg = _flagged_forward(lib, L, A, D, _anchors3(d, dtype, device))
+    flags = reg.cpu().tolist()
+    if dtype in (torch.float16, torch.bfloat16):
+        assert flags == [0] * 6
+    else:
+        assert flags == [1, 0, 0, 0, 0, 1]
+    ref = cufk.reconstruct(L, A, D, *_anchor_tensors(d, dtype, device).values())
+    assert torch.equal(xyz, ref)
+
+
+def test_far_chain_is_not_regular_in_fp32(cufk, device):
+    lib = _abi()
+    d = _inputs(2, 50, seed=22, anchors=True, dtype=torch.float32)
+    an = list(_anchors3(d, torch.float32, device))
+    L, A, D = (_dev(d[k], torch.float32, device) for k in ("lengths", "angles", "dihedrals"))
+    an[0] = torch.tensor([100.0, 0.0, 0.0], device=device)  # 100 nm > 256 * 0.12 nm
+    _, reg = _flagged_forward(lib, L, A, D, an)
+    assert reg.cpu().tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("N", [4, 5, 70, 259, 1028, 2049, 2051])
+def test_fast_and_exact_backward_agree(cufk, device, dtype, N):
+    lib = _abi()
+    d = _inputs(4, N, seed=300 + N, anchors=True, dtype=dtype)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    xyz, reg = _flagged_forward(lib, L, A, D, an)
+    assert reg.cpu().tolist() == [1] * 4
+    p = lambda t: t.data_ptr()  # noqa: E731
+    st = torch.cuda.current_stream().cuda_stream
+    fast = [torch.empty_like(t) for t in (L, A, D)]
+    exact = [torch.empty_like(t) for t in (L, A, D)]
+    assert lib.cufk_reconstruct_bwd_saved(_CODES[dtype], p(L), p(A), p(D), *map(p, an), p(xyz), p(reg), p(g),
+                                          *map(p, fast), 4, N, st) == 0
+    assert lib.cufk_reconstruct_bwd(_CODES[dtype], p(L), p(A), p(D), *map(p, an), p(g), *map(p, exact), 4, N, st) == 0
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    tol = 1e-9 if dtype == torch.float64 else 2e-4
+    for name, f, e, r in zip(("lengths", "angles", "dihedrals"), fast, exact, ref):
+        scale = max(1e-30, np.abs(r).max())
+        ef = np.abs(f.double().cpu().numpy() - r).max() / scale
+        ee = np.abs(e.double().cpu().numpy() - r).max() / scale
+        print(f"{dtype} N={N} d/d{name}: fast rel {ef:.2e}, exact rel {ee:.2e}")
+        assert ef <= tol and ee <= tol
+
+
+def test_inplace_modified_output_uses_exact_backward(cufk, device):
+    d = _inputs(3, 200, seed=23, anchors=True, dtype=torch.float64)
+    L, A, D = (_dev(d[k], torch.float64, device, True) for k in ("lengths", "angles", "dihedrals"))
+    xyz = cufk.reconstruct(L, A, D, *_anchor_tensors(d, torch.float64, device).values())
+    xyz.mul_(1.0)  # bumps the version counter; d(xyz)/d(xyz) is the identity
+    grads = torch.autograd.grad(xyz, (L, A, D), _dev(d["grad"], torch.float64, device))
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for got, want in zip(grads, ref):
+        assert np.abs(got.cpu().numpy() - want).max() <= 1e-9 * max(1.0, np.abs(want).max())
+
+
+def test_mixed_regular_and_irregular_batch(cufk, device):
+    d = _inputs(8, 600, seed=24, anchors=True, dtype=torch.float32)
+    d["lengths"][2, 100] *= -1
+    d["angles"][5, 300] = 0.1
+    _, grads = _run(cufk, d, torch.float32, device)
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for got, want in zip(grads, ref):
+        err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
+        print("per-chain rel err", err)
+        assert err.max() <= 2e-4
