@@ -6,14 +6,20 @@ chains (config 2 draws: lengths ~N(0.145, 0.01) clipped to [0.12, 0.17], angles 
 already resident in HBM.  The step runs through the public autograd API
 (``reconstruct`` + ``torch.autograd.grad``).
 
-Kernel-level figures come from HIP events recorded on the stream the kernels run on (the
-current torch stream, which the extension launches on) around back-to-back launches of each
-kernel through the C ABI.  ``roofline`` is for the backward kernel (the larger one): its
-algorithmic bytes per launch are 4*B*(9N-12) (read lengths, angles, dihedrals and grad_xyz,
-write the three gradients), against MI355X's 8 TB/s HBM peak.
+The timed steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB
+at config 2), so no step finds its inputs in the 256 MB last-level cache left behind by the
+previous one.  HIP events recorded inside the timed region on the stream the kernels run on
+(the current torch stream, which the extension launches on) bracket the K timed steps; a second
+pass of K steps with an event between forward and backward splits the step.  ``roofline`` is
+for the backward (the larger one): its algorithmic bytes per launch are 4*B*(9N-12) (read
+lengths, angles, dihedrals and grad_xyz, write the three gradients), divided by the average
+duration of the backward entry point the autograd path calls, timed through the C ABI over
+back-to-back launches rotating over the same input sets, against MI355X's 8 TB/s HBM peak.  ``traffic`` is the
+HBM bytes per launch the rocprofv3 FETCH_SIZE and WRITE_SIZE counters read for the same kernel,
+copied from the committed summaries under profiles/ (MEASURED_TRAFFIC below).
 
 The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host on a bounded
-sample of chains of the same shape, scaled to atoms/s.
+sample of chains of the same shape (128-chain chunks until about 15 s of work), scaled to atoms/s.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16]
 """
@@ -44,6 +50,13 @@ BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
 DTYPE_CODES = {"float32": 0, "float64": 1, "float16": 2, "bfloat16": 3}
 ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by what the
+# counter reads for a plain copy of known size; see profiles/reconstruct_c2_hbm_traffic.md.
+# Keyed by (config, kernel); a missing entry reports traffic as null.
+MEASURED_TRAFFIC = {
+    ("c2", "reconstruct_backward"): 303442035,  # 202614089 read (xyz, grad_xyz) + 100827947 written
+}
+
 
 def parse_args():
     p = argparse.ArgumentParser()
@@ -52,8 +65,10 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     p.add_argument("--kernel-reps", type=int, default=50)
+    p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = auto)")
+    p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = about 15 s of work)")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     return p.parse_args()
@@ -69,7 +84,7 @@ def copy_probe(mib):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    ms = event_time_ms(torch, lambda: dst.copy_(src), 10)
+    ms = event_time_ms(torch, lambda i: dst.copy_(src), 10)
     print(json.dumps({"copy_probe_mib": mib, "avg_us": ms * 1e3, "GBs_read_plus_write": 2 * n * 4 / (ms * 1e-3) / 1e9}))
     return 0
 
@@ -87,41 +102,59 @@ def synthetic(B, N, seed, torch, device, dtype):
 
 
 def event_time_ms(torch, fn, reps):
+    """Average time of fn(i) over reps back-to-back calls (i = 0..reps-1), HIP events on the
+    current stream."""
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    fn()
+    fn(0)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(reps):
-        fn()
+    for i in range(reps):
+        fn(i)
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) / reps
 
 
-def cpu_baseline(kind, B, N, sample):
-    """Float64 oracle on `sample` chains (fwd + bwd), scaled to atoms/s."""
+def cpu_baseline(kind, B, N, sample, seconds):
+    """Float64 oracle fwd + bwd on a bounded sample of chains, scaled to atoms/s.
+
+    Chains are processed in chunks of at most 128 (bounding memory).  With sample == 0,
+    chunks run until about `seconds` of work is done or B chains are covered; otherwise exactly
+    `sample` chains.  A 4-chain warm-up is not counted.
+    Returns (atoms/s, chains, wall seconds, cpu seconds)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import nerf64 as o
 
-    if kind == "torsion":
-        rng = np.random.default_rng(3)
-        raw = rng.normal(size=(sample, 2 * (N - 3)))
-        g = rng.normal(size=(sample, N, 3))
-        c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
-        t0 = time.perf_counter()
-        x = o.torsion_forward(raw, c)
-        o.torsion_backward(raw, x, g, c)
-        dt = time.perf_counter() - t0
-    else:
-        d = o.synthetic_inputs(sample, N, seed=2, anchors=True)
-        an = dict(p0=d["p0"], first_direction=d["first_direction"], initial_normal=d["initial_normal"])
-        t0 = time.perf_counter()
-        o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
-        o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **an)
-        dt = time.perf_counter() - t0
-    return sample * N / dt, dt
+    def chunk(n, seed):
+        if kind == "torsion":
+            rng = np.random.default_rng(seed)
+            raw = rng.normal(size=(n, 2 * (N - 3)))
+            g = rng.normal(size=(n, N, 3))
+            c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+            t0, c0 = time.perf_counter(), time.process_time()
+            x = o.torsion_forward(raw, c)
+            o.torsion_backward(raw, x, g, c)
+        else:
+            d = o.synthetic_inputs(n, N, seed=seed, anchors=True)
+            an = dict(p0=d["p0"], first_direction=d["first_direction"], initial_normal=d["initial_normal"])
+            t0, c0 = time.perf_counter(), time.process_time()
+            o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+            o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **an)
+        return time.perf_counter() - t0, time.process_time() - c0
+
+    chunk(4, 1000)
+    limit = sample if sample > 0 else B
+    wall = cpu = 0.0
+    done = 0
+    while done < limit and (sample > 0 or wall < seconds):
+        n = min(128, limit - done)
+        w, c = chunk(n, 2 + done)
+        wall += w
+        cpu += c
+        done += n
+    return done * N / wall, done, wall, cpu
 
 
 def main():
@@ -145,68 +178,50 @@ def main():
     dtype = getattr(torch, dtype_name)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    L, A, D, g, p0, fd, n0 = synthetic(B, N, 2, torch, device, dtype)
+    nsets = max(1, args.sets)
     s = ELEM_BYTES[dtype_name]
-
-    if kind == "reconstruct":
-        L.requires_grad_(True)
-        A.requires_grad_(True)
-        D.requires_grad_(True)
-
-        def step():
-            xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
-            return torch.autograd.grad(xyz, (L, A, D), g)
-
-        fwd_bytes = s * B * (6 * N - 6)
-        bwd_bytes = s * B * (9 * N - 12)
-    else:
-        gen = torch.Generator().manual_seed(3)
-        raw = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
-        raw.requires_grad_(True)
-        f = cufk_amd.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
-
-        def step():
-            xyz = f(raw)
-            return torch.autograd.grad(xyz, (raw,), g)
-
-        fwd_bytes = s * B * (5 * N - 6)
-        bwd_bytes = s * B * (10 * N - 12)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    t_start.record(stream)
-    for _ in range(args.steps):
-        step()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = t_start.elapsed_time(t_end) / args.steps
-
-    # Kernel-level timing through the C ABI (same library the extension links).
-    lib = ctypes.CDLL(str(cufk_amd._native.HIP_LIBRARY))
     code = DTYPE_CODES[dtype_name]
-    st = ctypes.c_void_p(stream.cuda_stream)
+    lib = ctypes.CDLL(str(cufk_amd._native.HIP_LIBRARY))  # the library the extension links
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     i64 = ctypes.c_int64
+
+    # One entry per input set: the autograd step and the two C-ABI calls it makes.
+    steps, fwds, bwds, regular = [], [], [], []
     if kind == "reconstruct":
-        xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
-        regular = torch.empty(B, device=device, dtype=torch.uint8)
-        gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+        fwd_bytes = s * B * (6 * N - 6)
+        bwd_bytes = s * B * (9 * N - 12)
+        for k in range(nsets):
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype)
+            L.requires_grad_(True)
+            A.requires_grad_(True)
+            D.requires_grad_(True)
 
-        # The entry points the autograd path uses: the flagged forward and the backward that
-        # takes the forward's output (position-based adjoint for regular chains).
-        def fwd():
-            rc = lib.cufk_reconstruct_fwd_flagged(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(regular),
-                                                  i64(B), i64(N), st)
-            assert rc == 0, rc
+            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
+                xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
+                if mark is not None:
+                    mark.record()
+                return torch.autograd.grad(xyz, (L, A, D), g)
 
-        def bwd():
-            rc = lib.cufk_reconstruct_bwd_saved(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(regular), P(g),
-                                                P(gL), P(gA), P(gD), i64(B), i64(N), st)
-            assert rc == 0, rc
+            xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+            flags = torch.empty(B, device=device, dtype=torch.uint8)
+            gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+
+            # The entry points the autograd path uses: the flagged forward and the backward
+            # that takes the forward's output (position-based adjoint for regular chains).
+            def fwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags):
+                rc = lib.cufk_reconstruct_fwd_flagged(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(flags),
+                                                      i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            def bwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, g=g, gL=gL, gA=gA, gD=gD):
+                rc = lib.cufk_reconstruct_bwd_saved(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(flags),
+                                                    P(g), P(gL), P(gA), P(gD), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            steps.append(step)
+            fwds.append(fwd)
+            bwds.append(bwd)
+            regular.append(flags)
     else:
         import math
 
@@ -215,25 +230,75 @@ def main():
 
         c = Consts((ctypes.c_float * 3)(*BOND_LENGTHS), (ctypes.c_double * 3)(*[math.sin(a) for a in BOND_ANGLES]),
                    (ctypes.c_double * 3)(*[math.cos(a) for a in BOND_ANGLES]))
-        xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
-        graw = torch.empty_like(raw)
+        f = cufk_amd.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+        fwd_bytes = s * B * (5 * N - 6)
+        bwd_bytes = s * B * (10 * N - 12)
+        for k in range(nsets):
+            gen = torch.Generator().manual_seed(3 + k)
+            raw = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
+            g = torch.randn(B, N, 3, generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
+            raw.requires_grad_(True)
 
-        def fwd():
-            rc = lib.cufk_torsion_fwd(code, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(xyz), i64(B), i64(N), st)
-            assert rc == 0, rc
+            def step(raw=raw, g=g, mark=None):
+                xyz = f(raw)
+                if mark is not None:
+                    mark.record()
+                return torch.autograd.grad(xyz, (raw,), g)
 
-        def bwd():
-            rc = lib.cufk_torsion_bwd(code, P(raw), i64(raw.stride(0)), P(xyz), P(g), P(graw), i64(graw.stride(0)),
-                                      ctypes.byref(c), i64(B), i64(N), st)
-            assert rc == 0, rc
+            xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+            graw = torch.empty_like(raw)
 
-    t_fwd = event_time_ms(torch, fwd, args.kernel_reps)
-    t_bwd = event_time_ms(torch, bwd, args.kernel_reps)
-    regular_frac = float(regular.float().mean()) if kind == "reconstruct" else None
+            def fwd(st, raw=raw, xyz=xyz):
+                rc = lib.cufk_torsion_fwd(code, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(xyz), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            def bwd(st, raw=raw, xyz=xyz, g=g, graw=graw):
+                rc = lib.cufk_torsion_bwd(code, P(raw), i64(raw.stride(0)), P(xyz), P(g), P(graw), i64(graw.stride(0)),
+                                          ctypes.byref(c), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            steps.append(step)
+            fwds.append(fwd)
+            bwds.append(bwd)
+
+    for i in range(args.warmup):
+        steps[i % nsets]()
+    torch.cuda.synchronize()
+
+    # Timed region: K steps back to back on the stream the kernels run on.
+    stream = torch.cuda.current_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    t_start, t_end = ev(), ev()
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(args.steps):
+        steps[i % nsets]()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    # The same K steps again with an event between each step's forward and backward (the
+    # extra event packets cost a few microseconds per step, so this pass is reported apart).
+    marks = [(ev(), ev()) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        marks[i][0].record(stream)
+        steps[i % nsets](mark=marks[i][1])
+    marks[args.steps][0].record(stream)
+    torch.cuda.synchronize()
+    seg_fwd = sum(marks[i][0].elapsed_time(marks[i][1]) for i in range(args.steps)) / args.steps
+    seg_bwd = sum(marks[i][1].elapsed_time(marks[i + 1][0]) for i in range(args.steps)) / args.steps
+
+    # Kernel-level timing straight through the C ABI, rotating over the same sets.
+    st = ctypes.c_void_p(stream.cuda_stream)
+    t_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.kernel_reps)
+    t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), args.kernel_reps)
+    regular_frac = float(torch.stack(regular).float().mean()) if regular else None
 
     atoms = B * N
     bw_bwd = bwd_bytes / (t_bwd * 1e-3) / 1e9
     bw_fwd = fwd_bytes / (t_fwd * 1e-3) / 1e9
+    traffic = MEASURED_TRAFFIC.get((args.config, f"{kind}_backward"))
     result = {
         "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
         "value": atoms / (ms_per_step * 1e-3),
@@ -248,7 +313,7 @@ def main():
         "dtype": {"float32": "f32", "float64": "f64", "float16": "f16", "bfloat16": "bf16"}[dtype_name],
         "data": "synthetic",
         "config": {"workload": f"{kind} fwd+bwd", "config": args.config, "batch": B, "points": N,
-                   "dtype": dtype_name, "anchors": "random"},
+                   "dtype": dtype_name, "anchors": "random", "input_sets": nsets},
         "roofline": {
             "bound": "hbm",
             "kernel": f"{kind}_backward",
@@ -256,29 +321,30 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": bw_bwd / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes": bwd_bytes,
             "avg_launch_us": t_bwd * 1e3,
         },
         "kernels": {
-            "forward_us": t_fwd * 1e3,
-            "backward_us": t_bwd * 1e3,
-            "forward_GBs": bw_fwd,
-            "fwd_plus_bwd_us": (t_fwd + t_bwd) * 1e3,
-            "fwd_plus_bwd_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / ((t_fwd + t_bwd) * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "fwd_plus_bwd_atoms_per_s": atoms / ((t_fwd + t_bwd) * 1e-3),
+            "step_forward_us": seg_fwd * 1e3,
+            "step_backward_us": seg_bwd * 1e3,
+            "abi_forward_us": t_fwd * 1e3,
+            "abi_backward_us": t_bwd * 1e3,
+            "abi_forward_GBs": bw_fwd,
+            "abi_backward_GBs": bw_bwd,
+            "step_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "regular_chain_fraction": regular_frac,
         },
     }
     if not args.no_cpu_baseline:
-        sample = args.cpu_sample or (64 if kind == "reconstruct" else 128)
-        v, dt = cpu_baseline(kind, B, N, sample)
+        v, chains, wall, cpu = cpu_baseline(kind, B, N, args.cpu_sample, args.cpu_seconds)
         result["cpu_baseline"] = {
             "value": v,
             "unit": "atoms/s",
-            "cores": 1,
+            "cores": max(1, round(cpu / wall)),
             "kind": "port",
-            "sample": f"float64 numpy oracle, fwd+bwd of {sample} chains x N={N} ({dt:.1f} s), scaled to atoms/s",
+            "sample": f"float64 numpy oracle, fwd+bwd of {chains} chains x N={N} ({wall:.1f} s wall, "
+                      f"{cpu:.1f} s cpu), scaled to atoms/s",
         }
     print(json.dumps(result))
     return 0

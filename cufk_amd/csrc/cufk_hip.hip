@@ -24,11 +24,14 @@ constexpr int kMaxSteps = 2048;  // block.cu:88, torsion.cu:97 (512 threads x 4 
 // ---------------------------------------------------------------------------- plans
 
 // (waves W, items per lane K), capacity 64*W*K steps; the smallest plan holding the chain.
+// Eight items per lane measured fastest at N = 2049 for both the forward and the
+// position-based backward (K = 16 runs out of registers and waves, K = 4 pays the lane scan
+// on too few items).
 template <typename Fn> int with_scan_plan(int steps, Fn&& fn) {
   if (steps <= 256) return fn.template operator()<1, 4>();
   if (steps <= 512) return fn.template operator()<1, 8>();
-  if (steps <= 1024) return fn.template operator()<1, 16>();
-  return fn.template operator()<2, 16>();
+  if (steps <= 1024) return fn.template operator()<2, 8>();
+  return fn.template operator()<4, 8>();
 }
 
 // The exact backward keeps per-step sin/cos in registers, so its K stays at 8.
@@ -91,8 +94,9 @@ int reconstruct_bwd_fast_typed(const T* xyz, const T* g, const uint8_t* regular,
                                hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_fast_kernel<T, W, K>), dim3(n), dim3(64 * W), 0, st, xyz + off * N * 3,
-                         g + off * N * 3, regular + off, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+      hipLaunchKernelGGL((reconstruct_backward_fast_kernel<T, W, K>), dim3(n), dim3(64 * W), 0, st,
+                         xyz + off * N * 3, g + off * N * 3, regular + off, gL + off * (N - 1), gA + off * (N - 2),
+                         gD + off * (N - 3), N);
     });
   });
 }

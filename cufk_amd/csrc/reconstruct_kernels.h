@@ -48,6 +48,7 @@ template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
 
 // x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v.  When
 // `regular` is non-null, regular[row] receives the fast-path predicate for the chain.
+// Rows are staged through LDS (coalesced 16-byte streams in and out).
 template <typename T, int W, int K>
 __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
@@ -70,6 +71,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int s0 = tid * K;
+  const int count = steps - s0 < K ? steps - s0 : K;  // items of this lane (may be <= 0)
 
   {
     R* const dst[3] = {stage, stage + Lay::kStepRow, stage + 2 * Lay::kStepRow};
@@ -88,6 +91,16 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     }
   }
   __syncthreads();
+  R lv[K], tv[K], pv[K];
+  {
+    const int b0 = Lay::lane_step_base(tid);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      lv[i] = stage[b0 + i];
+      tv[i] = stage[Lay::kStepRow + b0 + i];
+      pv[i] = stage[2 * Lay::kStepRow + b0 + i];
+    }
+  }
 
   // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
   // translation of the lane-local prefix after item i.
@@ -95,28 +108,23 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
-  const int s0 = tid * K;
-  const int b0 = Lay::lane_step_base(tid);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    if (s0 + i < steps) {
-      const R l = stage[b0 + i];
-      const R th = stage[Lay::kStepRow + b0 + i];
-      const R ph = stage[2 * Lay::kStepRow + b0 + i];
+    if (i < count) {
       double s, c, S, C;
-      sin_cos_wide(th, s, c);
-      sin_cos_wide(ph, S, C);
-      step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
-      ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
-      lmin = fmin(lmin, l);
+      sin_cos_wide(tv[i], s, c);
+      sin_cos_wide(pv[i], S, C);
+      step_forward(q.m, q.v, static_cast<double>(lv[i]), s, c, S, C);
+      ok = ok && lv[i] > R(0) && s >= FastPath<T>::kSinMin;
+      lmin = fmin(lmin, lv[i]);
     }
     y[i][0] = static_cast<R>(q.v[0]);
     y[i][1] = static_cast<R>(q.v[1]);
     y[i][2] = static_cast<R>(q.v[2]);
   }
 
-  // lane_carry's barrier also publishes base[] and retires every read of the step rows,
-  // which the point row below overwrites.
+  // lane_carry's barrier also publishes base[] and retires every read of the staged step
+  // rows, which the point row below overwrites.
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
   R F[9];
 #pragma unroll
@@ -133,21 +141,25 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
 
   R xmax = R(0);
-  const int o0 = Lay::lane_point_base(tid);
+  R xo[3 * K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    if (s0 + i < steps) {
-      const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
-      stage[o0 + 3 * i] = x.x;
-      stage[o0 + 3 * i + 1] = x.y;
-      stage[o0 + 3 * i + 2] = x.z;
-      xmax = abs_max3(xmax, x);
-    }
+    const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+    xo[3 * i] = x.x;
+    xo[3 * i + 1] = x.y;
+    xo[3 * i + 2] = x.z;
+    if (i < count) xmax = abs_max3(xmax, x);
   }
-  if (tid == 0) {
-    stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
-    stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
-    stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
+  {
+    const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+    for (int i = 0; i < 3 * K; ++i)
+      if (i < 3 * count) stage[o0 + i] = xo[i];
+    if (tid == 0) {
+      stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
+      stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
+      stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
+    }
   }
   if constexpr (FastPath<T>::kEnabled) {
     if (regular != nullptr) {
@@ -211,6 +223,15 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
   const int b0 = Lay::lane_step_base(tid);
   const int o0 = Lay::lane_point_base(tid);
 
+  if (skip != nullptr) {
+    // One flag per thread for the rows this workgroup strides over; leave at once when the
+    // fast kernel owns all of them (the common case: no launch-long chain of flag loads).
+    bool any = false;
+    for (int64_t row = blockIdx.x + static_cast<int64_t>(tid) * gridDim.x; row < batch;
+         row += static_cast<int64_t>(Lay::kLanes) * gridDim.x)
+      any = any || skip[row] == 0;
+    if (!__syncthreads_or(any)) return;
+  }
   for (int64_t row = blockIdx.x; row < batch; row += gridDim.x) {
     if (skip != nullptr && skip[row] != 0) continue;  // uniform across the workgroup
     const T* Lr = lengths + row * (points - 1);
@@ -345,6 +366,9 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
 //   T_j = M_j - x_{j-1} x F_j,  dL/dL[j-1] = u(b_{j-1}).F_j,
 //   dL/dA[j-2] = u(b_{j-1} x b_{j-2}).T_j,  dL/dD[j-3] = u(b_{j-2}).T_j,  b_i = x_{i+1} - x_i,
 // where F_j, M_j are suffix sums of g and x x g.  Positions are taken relative to x2.
+// Lane t owns points [3+tK, 3+tK+K) and writes the outputs of steps [tK, tK+K).
+// Rows are staged through LDS; each lane copies its points [tK, tK+K+3) and gradients into
+// registers, and its outputs replace its gradients in LDS for a coalesced store.
 template <typename T, int W, int K>
 __global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
     const T* __restrict__ xyz, const T* __restrict__ grad_xyz, const uint8_t* __restrict__ regular,
@@ -366,77 +390,93 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int s0 = tid * K;
+  const int count = steps - s0 < K ? steps - s0 : K;  // points of this lane (may be <= 0)
+  const int last = count - 1;
 
+  // xr holds points s0 .. s0+K+2 (point s0+j at 3j), gr the gradients of points 3+s0 ...
+  R xr[3 * K + 9], gr[3 * K];
+  V3<R> c;
   {
     R* const dst[2] = {xs, gs};
     const T* const src[2] = {Xr, Gr};
     load_point_rows<Lay, 2>(dst, src, points, tid);
+    __syncthreads();
+    c = load3(&xs[6]);
+    const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+    for (int i = 0; i < 3 * K; ++i) gr[i] = gs[o0 + i];
+    // Points s0 .. s0+2 precede the lane's own run (they belong to the previous lane or are
+    // points 0..2); points s0+3 .. sit in the lane's own slots.
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const V3<R> x = load3(&xs[Lay::point_slot(3 * (s0 + j))]);
+      xr[3 * j] = x.x;
+      xr[3 * j + 1] = x.y;
+      xr[3 * j + 2] = x.z;
+    }
+#pragma unroll
+    for (int i = 0; i < 3 * K; ++i) xr[9 + i] = xs[o0 + i];
   }
-  __syncthreads();
-
-  const V3<R> c = load3(&xs[6]);
-  auto pos = [&](int p) { return load3(&xs[Lay::point_slot(3 * p)]) - c; };
-  const int s0 = tid * K;
-  const int o0 = Lay::lane_point_base(tid);
-  const int last = (steps - s0 < K ? steps - s0 : K) - 1;  // last valid item of this lane
+  auto pos = [&](int j) { return V3<R>{xr[3 * j], xr[3 * j + 1], xr[3 * j + 2]} - c; };
 
   ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (i <= last) {
-      const V3<R> x = load3(&xs[o0 + 3 * i]) - c;
-      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      const V3<R> g = {gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]};
       lane_sum.f = lane_sum.f + g;
-      lane_sum.m = lane_sum.m + cross(x, g);
+      lane_sum.m = lane_sum.m + cross(pos(i + 3), g);
     }
   }
   const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
 
+  // Reverse walk: item i is point p = 3+s0+i (xr index i+3) with neighbours i+2, i+1.
   V3<R> F = tail.f, M = tail.m;
-  V3<R> xa, xb, xc, u1, b1;  // x_p, x_{p-1}, x_{p-2}; unit and raw bond p-1 -> p
-  if (last >= 0) {
-    const int p = 3 + s0 + last;
-    xa = pos(p);
-    xb = pos(p - 1);
-    xc = pos(p - 2);
-    b1 = xa - xb;
-    u1 = rsqrt_r(dot(b1, b1)) * b1;
-  }
+  R oL[K], oA[K], oD[K];
 #pragma unroll
   for (int i = K - 1; i >= 0; --i) {
     if (i <= last) {
-      const int p = 3 + s0 + i;
-      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      const V3<R> xa = pos(i + 3), xb = pos(i + 2), xc = pos(i + 1);
+      const V3<R> g = {gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]};
       F = F + g;
       M = M + cross(xa, g);
       const V3<R> Tq = M - cross(xb, F);
+      const V3<R> b1 = xa - xb;
       const V3<R> b2 = xb - xc;
-      const V3<R> u2 = rsqrt_r(dot(b2, b2)) * b2;
       const V3<R> n = cross(b1, b2);
-      gs[o0 + 3 * i] = dot(u1, F);
-      gs[o0 + 3 * i + 1] = dot(n, Tq) * rsqrt_r(dot(n, n));
-      gs[o0 + 3 * i + 2] = dot(u2, Tq);
-      xa = xb;
-      xb = xc;
-      xc = pos(p - 3);
-      b1 = b2;
-      u1 = u2;
+      oL[i] = dot(b1, F) * rsqrt_r(dot(b1, b1));
+      oA[i] = dot(n, Tq) * rsqrt_r(dot(n, n));
+      oD[i] = dot(b2, Tq) * rsqrt_r(dot(b2, b2));
     }
   }
   if (tid == 0) {
-    // Atoms 2 and 1: dL/dL[1], dL/dA[0] and dL/dL[0].  Here xa = x2 (the origin), xb = x1, xc = x0.
-    const V3<R> g2 = load3(&gs[6]);
+    // Atoms 2 and 1: dL/dL[1], dL/dA[0] and dL/dL[0]; x2 is the origin, so M_2 = M_3.
+    const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
     const V3<R> g1 = load3(&gs[3]);
+    const V3<R> g2 = load3(&gs[6]);
     F = F + g2;
-    const V3<R> Tq = M - cross(xb, F);
-    const V3<R> b2 = xb - xc;
-    const V3<R> n = cross(b1, b2);
-    gLr[1] = narrow<T>(dot(u1, F));
+    const V3<R> Tq = M - cross(x1, F);
+    const V3<R> b1 = x2 - x1;
+    const V3<R> b0 = x1 - x0;
+    const V3<R> n = cross(b1, b0);
+    gLr[1] = narrow<T>(dot(b1, F) * rsqrt_r(dot(b1, b1)));
     gAr[0] = narrow<T>(dot(n, Tq) * rsqrt_r(dot(n, n)));
-    gLr[0] = narrow<T>(dot(rsqrt_r(dot(b2, b2)) * b2, F + g1));
+    gLr[0] = narrow<T>(dot(b0, F + g1) * rsqrt_r(dot(b0, b0)));
   }
-  __syncthreads();
-  store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gs, steps, tid);
+  {
+    const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if (i <= last) {
+        gs[o0 + 3 * i] = oL[i];
+        gs[o0 + 3 * i + 1] = oA[i];
+        gs[o0 + 3 * i + 2] = oD[i];
+      }
+    }
+    __syncthreads();
+    store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gs, steps, tid);
+  }
 }
 
 }  // namespace cufk_amd
