@@ -21,7 +21,7 @@ namespace cufk_amd {
 // Storage types: float, double, _Float16 (torch.float16), __bf16 (torch.bfloat16).
 // Compute type: double for double, float otherwise.  Half types are widened on load and
 // rounded once on store (the reference instead rounds every payload operation to the
-// storage type, scalar.cuh:8-92; see the design notes for why this build does not).
+// storage type, scalar.cuh:8-92, which adds one storage-precision rounding per step).
 template <typename T> struct compute_type { using type = float; };
 template <> struct compute_type<double> { using type = double; };
 template <typename T> using compute_t = typename compute_type<T>::type;
@@ -33,41 +33,52 @@ template <typename T> __device__ __forceinline__ T narrow(compute_t<T> x) {
   return static_cast<T>(x);
 }
 
+// a * b + c for a constant c kept in a scalar register pair: one VOP3 v_fma_f64 (VOP3 reads
+// one scalar operand).  A plain fma with a 64-bit literal addend is emitted as the
+// two-address v_fmac with the literal first copied into two VGPRs, three VALU issues.
+__device__ __forceinline__ double fma_sk(double a, double b, double c) {
+  double d;
+  asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(c));
+  return d;
+}
+// c0 * u + c1 for constants c0, c1: v_mul_f64 and v_add_f64, each with a scalar operand.
+__device__ __forceinline__ double lin_sk(double u, double c0, double c1) {
+  double t, d;
+  asm("v_mul_f64 %0, %1, %2" : "=v"(t) : "v"(u), "s"(c0));
+  asm("v_add_f64 %0, %1, %2" : "=v"(d) : "v"(t), "s"(c1));
+  return d;
+}
+
 // sin and cos of a float argument evaluated in double: Cody-Waite reduction by pi/2 (two-part
-// constant) and Taylor polynomials through r^11 / r^12 (truncation < 1e-11 on |r| <= pi/4).
-// Rounded to float the results agree with correct rounding except in a few inputs per
-// million, so s^2 + c^2 - 1 has no systematic bias.  (The library sincosf carries a bias of
-// about -1.5e-8 in s^2 + c^2 that compounds into a scale drift along a 2000-step chain.)
-// FP64 FMA issues at the non-packed FP32 rate on CDNA3/4, so this costs about as much as the
-// float library routine.  |x| > 65536 and non-finite x take the library path.
+// constant), then near-minimax polynomials on |r| <= pi/4 (Chebyshev fits of
+// (sin r / r - 1) / r^2 and (cos r - 1) / r^2, degree 4 in r^2 each): |error| < 1.4e-14 for sin
+// and < 2.3e-13 for cos.  Rounded to float the results agree with correct rounding except in
+// a few inputs per million, so s^2 + c^2 - 1 has no systematic bias.  (The library sincosf
+// carries a bias of about -1.5e-8 in s^2 + c^2 that compounds into a scale drift along a
+// 2000-step chain.)  FP64 FMA issues at the non-packed FP32 rate on CDNA3/4.
+// |x| > 65536 and non-finite x take the library path.
 __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
-  if (!(fabsf(xf) <= 65536.0f)) {
-    sincos(static_cast<double>(xf), &s, &c);
-    return;
-  }
   const double x = xf;
   const double k = __builtin_rint(x * 0.63661977236758134308);
   double r = fma(-k, 1.5707963267948966, x);
   r = fma(-k, 6.123233995736766e-17, r);
-  const double r2 = r * r;
-  double ps = -2.505210838544172e-08;
-  ps = fma(ps, r2, 2.7557319223985893e-06);
-  ps = fma(ps, r2, -0.0001984126984126984);
-  ps = fma(ps, r2, 0.008333333333333333);
-  ps = fma(ps, r2, -0.16666666666666666);
-  const double sn = fma(r * r2, ps, r);
-  double pc = 2.08767569878681e-09;
-  pc = fma(pc, r2, -2.755731922398589e-07);
-  pc = fma(pc, r2, 2.48015873015873e-05);
-  pc = fma(pc, r2, -0.001388888888888889);
-  pc = fma(pc, r2, 0.041666666666666664);
-  pc = fma(pc, r2, -0.5);
-  const double cs = fma(r2, pc, 1.0);
+  const double u = r * r;
+  double ps = lin_sk(u, -2.4805636241834762e-08, 2.755599092956532e-06);
+  ps = fma_sk(ps, u, -0.00019841266916985966);
+  ps = fma_sk(ps, u, 0.008333333331079223);
+  ps = fma_sk(ps, u, -0.16666666666663885);
+  const double sn = fma(r * u, ps, r);
+  double pc = lin_sk(u, -2.7237140418016e-07, 2.4799862190148396e-05);
+  pc = fma_sk(pc, u, -0.00138888850913992);
+  pc = fma_sk(pc, u, 0.04166666663739607);
+  pc = fma_sk(pc, u, -0.4999999999996389);
+  const double cs = fma_sk(u, pc, 1.0);
   const int q = static_cast<int>(k) & 3;
   const double so = (q & 1) ? cs : sn;
   const double co = (q & 1) ? sn : cs;
   s = (q & 2) ? -so : so;
   c = ((q + 1) & 2) ? -co : co;
+  if (!(fabsf(xf) <= 65536.0f)) sincos(x, &s, &c);
 }
 __device__ __forceinline__ void sin_cos_wide(double x, double& s, double& c) { sincos(x, &s, &c); }
 

@@ -26,7 +26,9 @@ constexpr int kMaxSteps = 2048;  // block.cu:88, torsion.cu:97 (512 threads x 4 
 // (waves W, items per lane K), capacity 64*W*K steps; the smallest plan holding the chain.
 // Eight items per lane measured fastest at N = 2049 for both the forward and the
 // position-based backward (K = 16 runs out of registers and waves, K = 4 pays the lane scan
-// on too few items).
+// on too few items).  Both kernels stage rows with one word of padding per lane: at (4, 8)
+// that lets five forward workgroups (three backward) share a CU instead of four (two).
+constexpr int kScanPad = 1;
 template <typename Fn> int with_scan_plan(int steps, Fn&& fn) {
   if (steps <= 256) return fn.template operator()<1, 4>();
   if (steps <= 512) return fn.template operator()<1, 8>();
@@ -68,7 +70,7 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
                           uint8_t* regular, int64_t B, int N, hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_forward_kernel<T, W, K>), dim3(n), dim3(64 * W), 0, st, L + off * (N - 1),
+      hipLaunchKernelGGL((reconstruct_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st, L + off * (N - 1),
                          A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
                          regular ? regular + off : nullptr, N);
     });
@@ -94,7 +96,7 @@ int reconstruct_bwd_fast_typed(const T* xyz, const T* g, const uint8_t* regular,
                                hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_fast_kernel<T, W, K>), dim3(n), dim3(64 * W), 0, st,
+      hipLaunchKernelGGL((reconstruct_backward_fast_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          xyz + off * N * 3, g + off * N * 3, regular + off, gL + off * (N - 1), gA + off * (N - 2),
                          gD + off * (N - 3), N);
     });

@@ -49,13 +49,13 @@ template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
 // x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v.  When
 // `regular` is non-null, regular[row] receives the fast-path predicate for the chain.
 // Rows are staged through LDS (coalesced 16-byte streams in and out).
-template <typename T, int W, int K>
+template <typename T, int W, int K, int Pad = 4>
 __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
   using R = compute_t<T>;
-  using Lay = Layout<W, K>;
+  using Lay = Layout<W, K, Pad>;
   constexpr int kStage = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
   __shared__ __align__(16) R stage[kStage];
   __shared__ R wave_total[W][12];
@@ -91,19 +91,11 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     }
   }
   __syncthreads();
-  R lv[K], tv[K], pv[K];
-  {
-    const int b0 = Lay::lane_step_base(tid);
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      lv[i] = stage[b0 + i];
-      tv[i] = stage[Lay::kStepRow + b0 + i];
-      pv[i] = stage[2 * Lay::kStepRow + b0 + i];
-    }
-  }
 
   // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
-  // translation of the lane-local prefix after item i.
+  // translation of the lane-local prefix after item i.  Items are read from LDS as the scan
+  // reaches them, so only y stays in registers.
+  const int b0 = Lay::lane_step_base(tid);
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
   bool ok = true;
@@ -111,12 +103,13 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (i < count) {
+      const R l = stage[b0 + i];
       double s, c, S, C;
-      sin_cos_wide(tv[i], s, c);
-      sin_cos_wide(pv[i], S, C);
-      step_forward(q.m, q.v, static_cast<double>(lv[i]), s, c, S, C);
-      ok = ok && lv[i] > R(0) && s >= FastPath<T>::kSinMin;
-      lmin = fmin(lmin, lv[i]);
+      sin_cos_wide(stage[Lay::kStepRow + b0 + i], s, c);
+      sin_cos_wide(stage[2 * Lay::kStepRow + b0 + i], S, C);
+      step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+      ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
+      lmin = fmin(lmin, l);
     }
     y[i][0] = static_cast<R>(q.v[0]);
     y[i][1] = static_cast<R>(q.v[1]);
@@ -141,20 +134,18 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
 
   R xmax = R(0);
-  R xo[3 * K];
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-    const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
-    xo[3 * i] = x.x;
-    xo[3 * i + 1] = x.y;
-    xo[3 * i + 2] = x.z;
-    if (i < count) xmax = abs_max3(xmax, x);
-  }
   {
     const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
-    for (int i = 0; i < 3 * K; ++i)
-      if (i < 3 * count) stage[o0 + i] = xo[i];
+    for (int i = 0; i < K; ++i) {
+      if (i < count) {
+        const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+        stage[o0 + 3 * i] = x.x;
+        stage[o0 + 3 * i + 1] = x.y;
+        stage[o0 + 3 * i + 2] = x.z;
+        xmax = abs_max3(xmax, x);
+      }
+    }
     if (tid == 0) {
       stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
       stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
@@ -362,19 +353,19 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
 
 // ============================================================================ fast backward
 
-// Position-based adjoint for chains with regular[row] != 0 (A.6 of the design notes):
+// Position-based adjoint for chains with regular[row] != 0:
 //   T_j = M_j - x_{j-1} x F_j,  dL/dL[j-1] = u(b_{j-1}).F_j,
 //   dL/dA[j-2] = u(b_{j-1} x b_{j-2}).T_j,  dL/dD[j-3] = u(b_{j-2}).T_j,  b_i = x_{i+1} - x_i,
 // where F_j, M_j are suffix sums of g and x x g.  Positions are taken relative to x2.
 // Lane t owns points [3+tK, 3+tK+K) and writes the outputs of steps [tK, tK+K).
 // Rows are staged through LDS; each lane copies its points [tK, tK+K+3) and gradients into
 // registers, and its outputs replace its gradients in LDS for a coalesced store.
-template <typename T, int W, int K>
+template <typename T, int W, int K, int Pad = 4>
 __global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
     const T* __restrict__ xyz, const T* __restrict__ grad_xyz, const uint8_t* __restrict__ regular,
     T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points) {
   using R = compute_t<T>;
-  using Lay = Layout<W, K>;
+  using Lay = Layout<W, K, Pad>;
   __shared__ __align__(16) R xs[Lay::kPointRow];
   __shared__ __align__(16) R gs[Lay::kPointRow];  // upstream gradient, then the outputs
   __shared__ R wave_sum[W][6];

@@ -1,13 +1,17 @@
 // LDS staging of chain rows.
 //
 // Global rows are streamed with 16-byte vector accesses (coalesced across the workgroup) into
-// LDS layouts in which every lane's K steps (or K points) are contiguous and 16-byte aligned,
-// padded by 4 words per lane:
-//   step layout:  step s        -> slot s + 4*(s/K)              (lane stride K+4 words)
-//   point layout: flat xyz e>=9 -> slot 12 + e' + 4*(e'/(3K))    (e' = e-9, lane stride 3K+4)
+// LDS layouts in which every lane's K steps (or K points) are contiguous, padded by Pad words
+// per lane:
+//   step layout:  step s        -> slot s + Pad*(s/K)              (lane stride K+Pad)
+//   point layout: flat xyz e>=9 -> slot 12 + e' + Pad*(e'/(3K))    (e' = e-9, lane stride 3K+Pad)
 //                 e < 9 (points 0..2) -> slot e
-// Lane t owns steps [tK, tK+K) and points [3+tK, 3+tK+K).  With K a multiple of 4 the lane
-// strides are 4 mod 32 words, so the lanes' ds_read_b128 / ds_write_b128 hit disjoint banks.
+// Lane t owns steps [tK, tK+K) and points [3+tK, 3+tK+K).
+//   Pad = 4 (K a multiple of 4): lane runs are 16-byte aligned and the strides are 4 mod 32
+//     words, so ds_read_b128 / ds_write_b128 by the lanes hit disjoint banks.
+//   Pad = 1: odd strides, so one 32-bit access per lane hits 64 distinct banks; every access
+//     is a 32-bit one and the layout is 3/4 the size of Pad = 4 at K = 8 (more workgroups per
+//     CU where LDS bounds occupancy).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,21 +27,23 @@ typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 typedef double f64x2 __attribute__((ext_vector_type(2)));
 typedef double f64x2u __attribute__((ext_vector_type(2), aligned(8)));
 
-template <int W, int K> struct Layout {
+template <int W, int K, int Pad = 4> struct Layout {
   static_assert(K % 4 == 0, "lane segments must be whole 16-byte groups");
+  static_assert(Pad == 4 || Pad == 1, "padding is 4 words (vector LDS access) or 1 word");
   static constexpr int kWaves = W;
   static constexpr int kItems = K;
   static constexpr int kLanes = 64 * W;
   static constexpr int kCap = kLanes * K;  // steps per chain
-  static constexpr int kStepStride = K + 4;
+  static constexpr bool kVec = Pad == 4;    // lane runs 16-byte aligned
+  static constexpr int kStepStride = K + Pad;
   static constexpr int kStepRow = kLanes * kStepStride;
-  static constexpr int kPointStride = 3 * K + 4;
+  static constexpr int kPointStride = 3 * K + Pad;
   static constexpr int kPointRow = 12 + kLanes * kPointStride;
-  __device__ __forceinline__ static int step_slot(int s) { return s + 4 * (s / K); }
+  __device__ __forceinline__ static int step_slot(int s) { return s + Pad * (s / K); }
   __device__ __forceinline__ static int point_slot(int e) {
     if (e < 9) return e;
     const int t = e - 9;
-    return 12 + t + 4 * (t / (3 * K));
+    return 12 + t + Pad * (t / (3 * K));
   }
   __device__ __forceinline__ static int lane_step_base(int tid) { return tid * kStepStride; }
   __device__ __forceinline__ static int lane_point_base(int tid) { return 12 + tid * kPointStride; }
@@ -59,11 +65,26 @@ template <> struct Unit<double> {
   typedef f64x2 Local;
 };
 
+// A 16-byte group of consecutive LDS slots: one vector read when the layout keeps lane runs
+// 16-byte aligned, element reads otherwise.
+template <typename Lay, typename V, typename S> __device__ __forceinline__ V lds_vec(const S* p) {
+  if constexpr (Lay::kVec) {
+    return *reinterpret_cast<const V*>(p);
+  } else {
+    V v;
+#pragma unroll
+    for (int e = 0; e < static_cast<int>(sizeof(V) / sizeof(S)); ++e) v[e] = p[e];
+    return v;
+  }
+}
+
 // Rows of NR arrays into LDS: dst[r][slot(first + e)] = src[r][first + e] for e in [0, n).
 // Two-phase: every global load of the thread is issued into registers before the first LDS
 // write, so a workgroup pays one memory latency per staging phase, not one per group.
-// MaxN bounds n at compile time.
-template <int NR, int MaxN, int Lanes, typename T, typename SlotFn>
+// MaxN bounds n at compile time.  A 16-byte group never straddles a lane segment, so its
+// elements land in consecutive slots; Vec writes it with one vector LDS store (slots 16-byte
+// aligned), otherwise element by element.
+template <int NR, int MaxN, int Lanes, bool Vec, typename T, typename SlotFn>
 __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
                                            int tid, SlotFn slot) {
   using R = compute_t<T>;
@@ -91,7 +112,15 @@ __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const
       const int g = tid + j * Lanes;
       if (g < groups) {
 #pragma unroll
-        for (int r = 0; r < NR; ++r) *reinterpret_cast<typename Unit<T>::Local*>(dst[r] + slot(first + E * g)) = buf[r][j];
+        for (int r = 0; r < NR; ++r) {
+          R* const d = dst[r] + slot(first + E * g);
+          if constexpr (Vec) {
+            *reinterpret_cast<typename Unit<T>::Local*>(d) = buf[r][j];
+          } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) d[e] = buf[r][j][e];
+          }
+        }
       }
     }
     if (te < n) {
@@ -123,7 +152,7 @@ __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const
 // NR step rows (n <= kCap elements each) into step layouts.
 template <typename Lay, int NR, typename T>
 __device__ __forceinline__ void load_step_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int n, int tid) {
-  stage_rows<NR, Lay::kCap, Lay::kLanes, T>(dst, src, 0, n, tid, [](int s) { return Lay::step_slot(s); });
+  stage_rows<NR, Lay::kCap, Lay::kLanes, Lay::kVec, T>(dst, src, 0, n, tid, [](int s) { return Lay::step_slot(s); });
 }
 
 // NR (points, 3) rows into point layouts.
@@ -134,8 +163,8 @@ __device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], 
 #pragma unroll
     for (int r = 0; r < NR; ++r) dst[r][tid] = widen(src[r][tid]);
   }
-  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, T>(dst, src, 9, 3 * points - 9, tid,
-                                                [](int e) { return Lay::point_slot(e); });
+  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, T>(dst, src, 9, 3 * points - 9, tid,
+                                                           [](int e) { return Lay::point_slot(e); });
 }
 
 // dst[s] = src[step_slot(s)] for s in [0, n).
@@ -144,12 +173,12 @@ __device__ __forceinline__ void store_step_row(T* __restrict__ dst, const comput
   if constexpr (std::is_same_v<T, float>) {
     const int groups = n >> 2;
     for (int g = tid; g < groups; g += Lay::kLanes)
-      *reinterpret_cast<f32x4u*>(dst + 4 * g) = *reinterpret_cast<const f32x4*>(src + Lay::step_slot(4 * g));
+      *reinterpret_cast<f32x4u*>(dst + 4 * g) = lds_vec<Lay, f32x4>(src + Lay::step_slot(4 * g));
     for (int s = 4 * groups + tid; s < n; s += Lay::kLanes) dst[s] = src[Lay::step_slot(s)];
   } else if constexpr (std::is_same_v<T, double>) {
     const int groups = n >> 1;
     for (int g = tid; g < groups; g += Lay::kLanes)
-      *reinterpret_cast<f64x2u*>(dst + 2 * g) = *reinterpret_cast<const f64x2*>(src + Lay::step_slot(2 * g));
+      *reinterpret_cast<f64x2u*>(dst + 2 * g) = lds_vec<Lay, f64x2>(src + Lay::step_slot(2 * g));
     if ((n & 1) && tid == 0) dst[n - 1] = src[Lay::step_slot(n - 1)];
   } else {
     for (int s = tid; s < n; s += Lay::kLanes) dst[s] = narrow<T>(src[Lay::step_slot(s)]);
@@ -165,12 +194,12 @@ __device__ __forceinline__ void store_point_row(T* __restrict__ dst, const compu
   if constexpr (std::is_same_v<T, float>) {
     const int groups = n >> 2;
     for (int g = tid; g < groups; g += Lay::kLanes)
-      *reinterpret_cast<f32x4u*>(dst + 9 + 4 * g) = *reinterpret_cast<const f32x4*>(src + Lay::point_slot(9 + 4 * g));
+      *reinterpret_cast<f32x4u*>(dst + 9 + 4 * g) = lds_vec<Lay, f32x4>(src + Lay::point_slot(9 + 4 * g));
     for (int e = 4 * groups + tid; e < n; e += Lay::kLanes) dst[9 + e] = src[Lay::point_slot(9 + e)];
   } else if constexpr (std::is_same_v<T, double>) {
     const int groups = n >> 1;
     for (int g = tid; g < groups; g += Lay::kLanes)
-      *reinterpret_cast<f64x2u*>(dst + 9 + 2 * g) = *reinterpret_cast<const f64x2*>(src + Lay::point_slot(9 + 2 * g));
+      *reinterpret_cast<f64x2u*>(dst + 9 + 2 * g) = lds_vec<Lay, f64x2>(src + Lay::point_slot(9 + 2 * g));
     if ((n & 1) && tid == 0) dst[9 + n - 1] = src[Lay::point_slot(9 + n - 1)];
   } else {
     for (int e = tid; e < n; e += Lay::kLanes) dst[9 + e] = narrow<T>(src[Lay::point_slot(9 + e)]);
@@ -188,9 +217,9 @@ __device__ __forceinline__ void store_interleaved_rows(T* __restrict__ a, T* __r
     const int groups = steps >> 2;  // 4 steps never straddle a lane (K % 4 == 0)
     for (int g = tid; g < groups; g += Lay::kLanes) {
       const float* p = src + Lay::point_slot(9 + 12 * g);
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(p);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(p + 4);
-      const f32x4 v2 = *reinterpret_cast<const f32x4*>(p + 8);
+      const f32x4 v0 = lds_vec<Lay, f32x4>(p);
+      const f32x4 v1 = lds_vec<Lay, f32x4>(p + 4);
+      const f32x4 v2 = lds_vec<Lay, f32x4>(p + 8);
       *reinterpret_cast<f32x4u*>(a + 4 * g) = f32x4{v0.x, v0.w, v1.z, v2.y};
       *reinterpret_cast<f32x4u*>(b + 4 * g) = f32x4{v0.y, v1.x, v1.w, v2.z};
       *reinterpret_cast<f32x4u*>(c + 4 * g) = f32x4{v0.z, v1.y, v2.x, v2.w};
