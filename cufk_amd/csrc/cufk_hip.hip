@@ -26,18 +26,11 @@ constexpr int kMaxSteps = 2048;  // block.cu:88, torsion.cu:97 (512 threads x 4 
 // (waves W, items per lane K), capacity 64*W*K steps; the smallest plan holding the chain.
 // Eight items per lane measured fastest at N = 2049 for both the forward and the
 // position-based backward (K = 16 runs out of registers and waves, K = 4 pays the lane scan
-// on too few items).  Both kernels stage rows with one word of padding per lane: at (4, 8)
-// that lets five forward workgroups (three backward) share a CU instead of four (two).
+// on too few items).  The exact backward uses the same plans.  The kernels stage rows with one
+// word of padding per lane: at (4, 8) that lets five forward workgroups (three backward)
+// share a CU instead of four (two).
 constexpr int kScanPad = 1;
 template <typename Fn> int with_scan_plan(int steps, Fn&& fn) {
-  if (steps <= 256) return fn.template operator()<1, 4>();
-  if (steps <= 512) return fn.template operator()<1, 8>();
-  if (steps <= 1024) return fn.template operator()<2, 8>();
-  return fn.template operator()<4, 8>();
-}
-
-// The exact backward keeps per-step sin/cos in registers, so its K stays at 8.
-template <typename Fn> int with_exact_plan(int steps, Fn&& fn) {
   if (steps <= 256) return fn.template operator()<1, 4>();
   if (steps <= 512) return fn.template operator()<1, 8>();
   if (steps <= 1024) return fn.template operator()<2, 8>();
@@ -77,28 +70,31 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
   });
 }
 
-// Exact backward for every chain (skip == nullptr) or for the chains with skip[row] == 0;
-// the kernel strides over chains, so any grid size covers the batch.
+// Exact backward for every chain; the kernel strides over chains, so any grid size covers
+// the batch.
 template <typename T>
 int reconstruct_bwd_exact_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* g,
-                                T* gL, T* gA, T* gD, const uint8_t* skip, int64_t B, int N, hipStream_t st) {
-  return with_exact_plan(N - 3, [&]<int W, int K>() {
-    const int64_t cap = skip ? 256 : 65536;
+                                T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    const int64_t cap = 65536;
     const unsigned grid = static_cast<unsigned>(B < cap ? B : cap);
-    hipLaunchKernelGGL((reconstruct_backward_exact_kernel<T, W, K>), dim3(grid), dim3(64 * W), 0, st, L, A, D, p0, fd,
-                       n0, g, gL, gA, gD, skip, N, static_cast<int>(B));
+    hipLaunchKernelGGL((reconstruct_backward_exact_kernel<T, W, K, kScanPad>), dim3(grid), dim3(64 * W), 0, st, L, A, D, p0, fd,
+                       n0, g, gL, gA, gD, N, static_cast<int>(B));
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
   });
 }
 
+// Backward over the saved forward output: one launch, each chain taking the position-based
+// or the exact path by its flag.
 template <typename T>
-int reconstruct_bwd_fast_typed(const T* xyz, const T* g, const uint8_t* regular, T* gL, T* gA, T* gD, int64_t B, int N,
-                               hipStream_t st) {
+int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
+                                const T* xyz, const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N,
+                                hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_fast_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
-                         xyz + off * N * 3, g + off * N * 3, regular + off, gL + off * (N - 1), gA + off * (N - 2),
-                         gD + off * (N - 3), N);
+      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
+                         regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
     });
   });
 }
@@ -207,8 +203,8 @@ int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, con
   return dispatch(dtype, [&]<typename T>() {
     return reconstruct_bwd_exact_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
                                           cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
-                                          mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), nullptr,
-                                          batch, N, st);
+                                          mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N,
+                                          st);
   });
 }
 
@@ -227,14 +223,17 @@ int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angle
   auto st = static_cast<hipStream_t>(stream);
   return dispatch(dtype, [&]<typename T>() {
     if constexpr (FastPath<T>::kEnabled) {
-      const int status = reconstruct_bwd_fast_typed<T>(cp<T>(xyz), cp<T>(grad_xyz), chain_regular, mp<T>(grad_lengths),
-                                                       mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N, st);
-      if (status != CUFK_OK) return status;
+      return reconstruct_bwd_saved_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                            cp<T>(first_direction), cp<T>(initial_normal), cp<T>(xyz), chain_regular,
+                                            cp<T>(grad_xyz), mp<T>(grad_lengths), mp<T>(grad_angles),
+                                            mp<T>(grad_dihedrals), batch, N, st);
+    } else {
+      // float16 / bfloat16 chains are never flagged regular.
+      return reconstruct_bwd_exact_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                            cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
+                                            mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N,
+                                            st);
     }
-    return reconstruct_bwd_exact_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
-                                          cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
-                                          mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals),
-                                          FastPath<T>::kEnabled ? chain_regular : nullptr, batch, N, st);
   });
 }
 

@@ -3,9 +3,9 @@
 // One workgroup of W wave64s per chain; lane t owns steps [tK, tK+K) (point s+3 for step s).
 //   reconstruct_forward_kernel     block_forward_kernel (block.cu:157-204)
 //   reconstruct_backward_exact     block_backward_kernel (block.cu:230-313): recomputes the frames
-//   reconstruct_backward_fast      the world-frame force/moment adjoint over the saved positions
-//                                  (the form torsion.cu:204-217 uses), for chains the forward
-//                                  marked regular
+//   reconstruct_backward_saved     the world-frame force/moment adjoint over the saved positions
+//                                  (the form torsion.cu:204-217 uses) for chains the forward
+//                                  marked regular, the exact recompute for the others
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -186,26 +186,27 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
 
 // ============================================================================ exact backward
 
-// World-frame adjoint with exact frame axes, recomputing the forward scan from the
-// parameters (valid for every finite input):
+// World-frame adjoint with exact frame axes for one chain, recomputing the forward scan from
+// the parameters (valid for every finite input):
 //   F_i = sum_{j>=i} g_j,  M_i = sum_{j>=i} x_j x g_j,  tau = M_{k+3} - x_{k+2} x F_{k+3}
 //   dL/dL[k+2] = R_k[:,0].F_{k+3},  dL/dA[k+1] = -R_k[:,2].tau,  dL/dD[k] = R_{k-1}[:,0].tau
 // with R_k the world rotation after step k; first-frame terms restate block.cu:206-228.
-// Positions are relative to x2 (the moments are translation invariant).  Grid-stride over
-// chains; chains with skip[row] != 0 are left to the fast kernel.
-template <typename T, int W, int K>
-__global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
-    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
-    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
-    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, const uint8_t* __restrict__ skip, int points, int batch) {
+// Positions are relative to x2 (the moments are translation invariant).  Every thread of
+// the workgroup calls this; pstage holds 3 step rows, gstage one point row.  The reverse walk
+// recomputes each step's sin/cos instead of keeping them in registers, so this path does not
+// raise the register count of a kernel that also carries the position-based path.
+template <typename T, typename Lay>
+__device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
+                                            const T* __restrict__ Dr, const T* __restrict__ p0,
+                                            const T* __restrict__ first_direction,
+                                            const T* __restrict__ initial_normal, const T* __restrict__ Gr,
+                                            T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
+                                            compute_t<T>* pstage, compute_t<T>* gstage,
+                                            compute_t<T> (&wave_total)[Lay::kWaves][12],
+                                            compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
   using R = compute_t<T>;
-  using Lay = Layout<W, K>;
-  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];  // parameters
-  __shared__ __align__(16) R gstage[Lay::kPointRow];     // upstream gradient, then the outputs
-  __shared__ R wave_total[W][12];
-  __shared__ R wave_sum[W][6];
-
+  constexpr int W = Lay::kWaves;
+  constexpr int K = Lay::kItems;
   const int steps = points - 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -213,171 +214,160 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
   const int s0 = tid * K;
   const int b0 = Lay::lane_step_base(tid);
   const int o0 = Lay::lane_point_base(tid);
-
-  if (skip != nullptr) {
-    // One flag per thread for the rows this workgroup strides over; leave at once when the
-    // fast kernel owns all of them (the common case: no launch-long chain of flag loads).
-    bool any = false;
-    for (int64_t row = blockIdx.x + static_cast<int64_t>(tid) * gridDim.x; row < batch;
-         row += static_cast<int64_t>(Lay::kLanes) * gridDim.x)
-      any = any || skip[row] == 0;
-    if (!__syncthreads_or(any)) return;
+  {
+    R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
+    const T* const src[3] = {Lr + 2, Ar + 1, Dr};
+    load_step_rows<Lay, 3>(dst, src, steps, tid);
+    R* const gdst[1] = {gstage};
+    const T* const gsrc[1] = {Gr};
+    load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
   }
+  const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+  __syncthreads();
+
+  // Pass 1: lane-local scan (double); Y = sum_i y_i g_i^T and sum_i g_i.
+  Rigid<double> qd = rigid_identity<double>();
+  R Y[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) Y[i] = R(0);
+  V3<R> gsum = {R(0), R(0), R(0)};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (s0 + i < steps) {
+      const R l = pstage[b0 + i];
+      double s, c, S, C;
+      sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
+      sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+      step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
+      const V3<R> g = load3(&gstage[o0 + 3 * i]);
+      const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        Y[3 * a + 0] += yv[a] * g.x;
+        Y[3 * a + 1] += yv[a] * g.y;
+        Y[3 * a + 2] += yv[a] * g.z;
+      }
+      gsum = gsum + g;
+    }
+  }
+
+  const Rigid<R> q = narrow_rigid<R>(qd);
+  const Rigid<R> excl = lane_carry<R, W>(q, wave_total, lane, wave);
+
+  // World frame at the lane start, origin at x2: R0 = F excl.m, X0 = F excl.v.
+  R R0[9];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      R0[3 * r + c] = ff.frame[3 * r] * excl.m[c] + ff.frame[3 * r + 1] * excl.m[3 + c] + ff.frame[3 * r + 2] * excl.m[6 + c];
+  }
+  const V3<R> X0 = rot_apply(ff.frame, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+
+  // Lane moment sum_i (X0 + R0 y_i) x g_i = X0 x gsum + axial part of R0 Y.
+  R Z[9];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) Z[3 * r + c] = R0[3 * r] * Y[c] + R0[3 * r + 1] * Y[3 + c] + R0[3 * r + 2] * Y[6 + c];
+  }
+  ForceMoment<R> lane_sum;
+  lane_sum.f = gsum;
+  lane_sum.m = cross(X0, gsum) + V3<R>{Z[5] - Z[7], Z[6] - Z[2], Z[1] - Z[3]};
+
+  // World state after the lane's last step.
+  R Rm[9];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) Rm[3 * r + c] = R0[3 * r] * q.m[c] + R0[3 * r + 1] * q.m[3 + c] + R0[3 * r + 2] * q.m[6 + c];
+  }
+  V3<R> x = X0 + rot_apply(R0, V3<R>{q.v[0], q.v[1], q.v[2]});
+
+  const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
+
+  // Pass 2: walk the lane's steps backwards; the outputs of step s replace g_{s+3} in LDS.
+  V3<R> Fs = tail.f, Ms = tail.m;
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    if (s0 + i < steps) {
+      const V3<R> g = load3(&gstage[o0 + 3 * i]);
+      Fs = Fs + g;
+      Ms = Ms + cross(x, g);
+      const R l = pstage[b0 + i];
+      const V3<R> col0 = {Rm[0], Rm[3], Rm[6]};
+      const V3<R> col2 = {Rm[2], Rm[5], Rm[8]};
+      const V3<R> xp = x - l * col0;
+      const V3<R> tau = Ms - cross(xp, Fs);
+      const R gl = dot(col0, Fs);
+      const R ga = -dot(col2, tau);
+      double s, c, S, C;
+      sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
+      sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+      step_backward(Rm, static_cast<R>(s), static_cast<R>(c), static_cast<R>(S), static_cast<R>(C));
+      const R gd = dot(V3<R>{Rm[0], Rm[3], Rm[6]}, tau);
+      gstage[o0 + 3 * i] = gl;
+      gstage[o0 + 3 * i + 1] = ga;
+      gstage[o0 + 3 * i + 2] = gd;
+      x = xp;
+    }
+  }
+  if (tid == 0) {
+    // First-frame parameters (block.cu:206-228); x2 is the origin, so M_2 = M_3.
+    const V3<R> g1 = load3(&gstage[3]);
+    const V3<R> g2 = load3(&gstage[6]);
+    const V3<R> F2 = Fs + g2;
+    const V3<R> x1 = ff.p1 - ff.p2;
+    const V3<R> tau2 = Ms - cross(x1, F2);
+    gLr[0] = narrow<T>(dot(ff.d0, F2 + g1));
+    gLr[1] = narrow<T>(dot(ff.d1, F2));
+    gAr[0] = narrow<T>(-dot(cross(ff.d0, ff.t0), tau2));
+  }
+  __syncthreads();
+  store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gstage, steps, tid);
+}
+
+// Exact backward for every chain; the workgroups stride over the batch.
+template <typename T, int W, int K, int Pad = 4>
+__global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
+    T* __restrict__ grad_dihedrals, int points, int batch) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K, Pad>;
+  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];  // parameters
+  __shared__ __align__(16) R gstage[Lay::kPointRow];     // upstream gradient, then the outputs
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
   for (int64_t row = blockIdx.x; row < batch; row += gridDim.x) {
-    if (skip != nullptr && skip[row] != 0) continue;  // uniform across the workgroup
-    const T* Lr = lengths + row * (points - 1);
-    const T* Ar = angles + row * (points - 2);
-    const T* Dr = dihedrals + row * (points - 3);
-    const T* Gr = grad_xyz + row * points * 3;
-    T* gLr = grad_lengths + row * (points - 1);
-    T* gAr = grad_angles + row * (points - 2);
-    T* gDr = grad_dihedrals + row * (points - 3);
-
-    {
-      R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
-      const T* const src[3] = {Lr + 2, Ar + 1, Dr};
-      load_step_rows<Lay, 3>(dst, src, steps, tid);
-      R* const gdst[1] = {gstage};
-      const T* const gsrc[1] = {Gr};
-      load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
-    }
-    const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-    __syncthreads();
-
-    // Pass 1: lane-local scan (double); keep sin/cos; Y = sum_i y_i g_i^T and sum_i g_i.
-    Rigid<double> qd = rigid_identity<double>();
-    R sc[K][4];
-    R Y[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) Y[i] = R(0);
-    V3<R> gsum = {R(0), R(0), R(0)};
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      sc[i][0] = sc[i][1] = sc[i][2] = sc[i][3] = R(0);
-      if (s0 + i < steps) {
-        const R l = pstage[b0 + i];
-        double s, c, S, C;
-        sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
-        sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
-        sc[i][0] = static_cast<R>(s);
-        sc[i][1] = static_cast<R>(c);
-        sc[i][2] = static_cast<R>(S);
-        sc[i][3] = static_cast<R>(C);
-        step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
-        const V3<R> g = load3(&gstage[o0 + 3 * i]);
-        const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-          Y[3 * a + 0] += yv[a] * g.x;
-          Y[3 * a + 1] += yv[a] * g.y;
-          Y[3 * a + 2] += yv[a] * g.z;
-        }
-        gsum = gsum + g;
-      }
-    }
-
-    const Rigid<R> q = narrow_rigid<R>(qd);
-    const Rigid<R> excl = lane_carry<R, W>(q, wave_total, lane, wave);
-
-    // World frame at the lane start, origin at x2: R0 = F excl.m, X0 = F excl.v.
-    R R0[9];
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-#pragma unroll
-      for (int c = 0; c < 3; ++c)
-        R0[3 * r + c] = ff.frame[3 * r] * excl.m[c] + ff.frame[3 * r + 1] * excl.m[3 + c] + ff.frame[3 * r + 2] * excl.m[6 + c];
-    }
-    const V3<R> X0 = rot_apply(ff.frame, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
-
-    // Lane moment sum_i (X0 + R0 y_i) x g_i = X0 x gsum + axial part of R0 Y.
-    R Z[9];
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-#pragma unroll
-      for (int c = 0; c < 3; ++c) Z[3 * r + c] = R0[3 * r] * Y[c] + R0[3 * r + 1] * Y[3 + c] + R0[3 * r + 2] * Y[6 + c];
-    }
-    ForceMoment<R> lane_sum;
-    lane_sum.f = gsum;
-    lane_sum.m = cross(X0, gsum) + V3<R>{Z[5] - Z[7], Z[6] - Z[2], Z[1] - Z[3]};
-
-    // World state after the lane's last step.
-    R Rm[9];
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-#pragma unroll
-      for (int c = 0; c < 3; ++c) Rm[3 * r + c] = R0[3 * r] * q.m[c] + R0[3 * r + 1] * q.m[3 + c] + R0[3 * r + 2] * q.m[6 + c];
-    }
-    V3<R> x = X0 + rot_apply(R0, V3<R>{q.v[0], q.v[1], q.v[2]});
-
-    const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
-
-    // Pass 2: walk the lane's steps backwards; the outputs of step s replace g_{s+3} in LDS.
-    V3<R> Fs = tail.f, Ms = tail.m;
-#pragma unroll
-    for (int i = K - 1; i >= 0; --i) {
-      if (s0 + i < steps) {
-        const V3<R> g = load3(&gstage[o0 + 3 * i]);
-        Fs = Fs + g;
-        Ms = Ms + cross(x, g);
-        const R l = pstage[b0 + i];
-        const V3<R> col0 = {Rm[0], Rm[3], Rm[6]};
-        const V3<R> col2 = {Rm[2], Rm[5], Rm[8]};
-        const V3<R> xp = x - l * col0;
-        const V3<R> tau = Ms - cross(xp, Fs);
-        const R gl = dot(col0, Fs);
-        const R ga = -dot(col2, tau);
-        step_backward(Rm, sc[i][0], sc[i][1], sc[i][2], sc[i][3]);
-        const R gd = dot(V3<R>{Rm[0], Rm[3], Rm[6]}, tau);
-        gstage[o0 + 3 * i] = gl;
-        gstage[o0 + 3 * i + 1] = ga;
-        gstage[o0 + 3 * i + 2] = gd;
-        x = xp;
-      }
-    }
-    if (tid == 0) {
-      // First-frame parameters (block.cu:206-228); x2 is the origin, so M_2 = M_3.
-      const V3<R> g1 = load3(&gstage[3]);
-      const V3<R> g2 = load3(&gstage[6]);
-      const V3<R> F2 = Fs + g2;
-      const V3<R> x1 = ff.p1 - ff.p2;
-      const V3<R> tau2 = Ms - cross(x1, F2);
-      gLr[0] = narrow<T>(dot(ff.d0, F2 + g1));
-      gLr[1] = narrow<T>(dot(ff.d1, F2));
-      gAr[0] = narrow<T>(-dot(cross(ff.d0, ff.t0), tau2));
-    }
-    __syncthreads();
-    store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gstage, steps, tid);
+    exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
+                        first_direction, initial_normal, grad_xyz + row * points * 3,
+                        grad_lengths + row * (points - 1), grad_angles + row * (points - 2),
+                        grad_dihedrals + row * (points - 3), pstage, gstage, wave_total, wave_sum, points);
     __syncthreads();  // the next chain's loads overwrite the staging rows
   }
 }
 
-// ============================================================================ fast backward
+// ============================================================================ position-based backward
 
-// Position-based adjoint for chains with regular[row] != 0:
+// Position-based adjoint for one chain the forward marked regular:
 //   T_j = M_j - x_{j-1} x F_j,  dL/dL[j-1] = u(b_{j-1}).F_j,
 //   dL/dA[j-2] = u(b_{j-1} x b_{j-2}).T_j,  dL/dD[j-3] = u(b_{j-2}).T_j,  b_i = x_{i+1} - x_i,
-// where F_j, M_j are suffix sums of g and x x g.  Positions are taken relative to x2.
-// Lane t owns points [3+tK, 3+tK+K) and writes the outputs of steps [tK, tK+K).
-// Rows are staged through LDS; each lane copies its points [tK, tK+K+3) and gradients into
-// registers, and its outputs replace its gradients in LDS for a coalesced store.
-template <typename T, int W, int K, int Pad = 4>
-__global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
-    const T* __restrict__ xyz, const T* __restrict__ grad_xyz, const uint8_t* __restrict__ regular,
-    T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points) {
+// where F_j, M_j are suffix sums of g and x x g and u(v) = v/|v|.  Positions are taken
+// relative to x2.  Lane t owns points [3+tK, 3+tK+K) and writes the outputs of steps
+// [tK, tK+K).  Rows are staged through LDS (xs, gs: one point row each); each lane copies its
+// points [tK, tK+K+3) and gradients into registers, and its outputs replace its gradients in
+// LDS for a coalesced store.
+template <typename T, typename Lay>
+__device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T* __restrict__ Gr,
+                                               T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
+                                               compute_t<T>* xs, compute_t<T>* gs,
+                                               compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
   using R = compute_t<T>;
-  using Lay = Layout<W, K, Pad>;
-  __shared__ __align__(16) R xs[Lay::kPointRow];
-  __shared__ __align__(16) R gs[Lay::kPointRow];  // upstream gradient, then the outputs
-  __shared__ R wave_sum[W][6];
-
-  const int64_t row = blockIdx.x;
-  if (regular[row] == 0) return;  // the exact kernel handles this chain
+  constexpr int W = Lay::kWaves;
+  constexpr int K = Lay::kItems;
   const int steps = points - 3;
-  const T* Xr = xyz + row * points * 3;
-  const T* Gr = grad_xyz + row * points * 3;
-  T* gLr = grad_lengths + row * (points - 1);
-  T* gAr = grad_angles + row * (points - 2);
-  T* gDr = grad_dihedrals + row * (points - 3);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -467,6 +457,37 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_fast_kernel(
     }
     __syncthreads();
     store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gs, steps, tid);
+  }
+}
+
+// Backward given the forward's own output: one workgroup per chain, the position-based
+// adjoint for chains with regular[row] != 0 and the exact recompute for the others, in one
+// launch.  The two paths share the LDS: region A holds xs or the parameter rows, region B
+// the gradient row.
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
+    T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K, Pad>;
+  constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R region_a[kA];
+  __shared__ __align__(16) R region_b[Lay::kPointRow];
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
+  const int64_t row = blockIdx.x;
+  T* gLr = grad_lengths + row * (points - 1);
+  T* gAr = grad_angles + row * (points - 2);
+  T* gDr = grad_dihedrals + row * (points - 3);
+  if (regular[row] != 0) {
+    position_chain<T, Lay>(xyz + row * points * 3, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a, region_b,
+                           wave_sum, points);
+  } else {
+    exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
+                        first_direction, initial_normal, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a,
+                        region_b, wave_total, wave_sum, points);
   }
 }
 
