@@ -6,6 +6,8 @@ chains (config 2 draws: lengths ~N(0.145, 0.01) clipped to [0.12, 0.17], angles 
 already resident in HBM.  The step runs through the public autograd API
 (``reconstruct`` + ``torch.autograd.grad``).
 
+The default 1000 warm-up steps (about 0.1 s of GPU work at config 2) bring the GPU to its
+steady clocks: after only 10 warm-up steps the first 50 timed steps run about 20 % slower.
 The timed steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB
 at config 2), so no step finds its inputs in the 256 MB last-level cache left behind by the
 previous one.  HIP events recorded inside the timed region on the stream the kernels run on
@@ -61,10 +63,10 @@ MEASURED_TRAFFIC = {
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=500)
+    p.add_argument("--warmup", type=int, default=1000)
     p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    p.add_argument("--kernel-reps", type=int, default=50)
+    p.add_argument("--kernel-reps", type=int, default=200)
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = about 15 s of work)")

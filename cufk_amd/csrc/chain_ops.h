@@ -49,6 +49,10 @@ __device__ __forceinline__ double lin_sk(double u, double c0, double c1) {
   return d;
 }
 
+// Largest |x| the reduction in sin_cos_wide handles; beyond it (and for infinities) the
+// library routine takes over.
+constexpr float kWideReduceMax = 65536.0f;
+
 // sin and cos of a float argument evaluated in double: Cody-Waite reduction by pi/2 (two-part
 // constant), then near-minimax polynomials on |r| <= pi/4 (Chebyshev fits of
 // (sin r / r - 1) / r^2 and (cos r - 1) / r^2, degree 4 in r^2 each): |error| < 1.4e-14 for sin
@@ -56,7 +60,10 @@ __device__ __forceinline__ double lin_sk(double u, double c0, double c1) {
 // a few inputs per million, so s^2 + c^2 - 1 has no systematic bias.  (The library sincosf
 // carries a bias of about -1.5e-8 in s^2 + c^2 that compounds into a scale drift along a
 // 2000-step chain.)  FP64 FMA issues at the non-packed FP32 rate on CDNA3/4.
-// |x| > 65536 and non-finite x take the library path.
+// With Checked, |x| > kWideReduceMax takes the library path; kernels that have verified the
+// range of a whole chain beforehand call the unchecked form, which keeps the library code out
+// of their unrolled loops.  NaN gives NaN on either path.
+template <bool Checked = true>
 __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
   const double x = xf;
   const double k = __builtin_rint(x * 0.63661977236758134308);
@@ -78,9 +85,16 @@ __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
   const double co = (q & 1) ? sn : cs;
   s = (q & 2) ? -so : so;
   c = ((q + 1) & 2) ? -co : co;
-  if (!(fabsf(xf) <= 65536.0f)) sincos(x, &s, &c);
+  if constexpr (Checked) {
+    if (fabsf(xf) > kWideReduceMax) sincos(x, &s, &c);
+  }
 }
+template <bool Checked = true>
 __device__ __forceinline__ void sin_cos_wide(double x, double& s, double& c) { sincos(x, &s, &c); }
+
+// True when sin_cos_wide<true> would leave its polynomial path for x.
+__device__ __forceinline__ bool beyond_wide_reduce(float x) { return fabsf(x) > kWideReduceMax; }
+__device__ __forceinline__ bool beyond_wide_reduce(double) { return false; }
 
 // Unit (sin, cos) from a raw pair in double (torsion.cu:119-141 clamps rs^2 + rc^2 at 1e-16).
 template <typename R> __device__ __forceinline__ void pair_unit(R rs, R rc, double& S, double& C) {
@@ -279,6 +293,18 @@ template <typename R> __device__ __forceinline__ Rigid<R> wave_prefix(Rigid<R> x
   x = compose(dpp_rigid<kRowBcast15, 0xa>(x), x);
   x = compose(dpp_rigid<kRowBcast31, 0xc>(x), x);
   return x;
+}
+
+// OR of a predicate over the workgroup: one vote per wave into flags[], then a barrier.
+// Uses W words of LDS (the compiler's __syncthreads_or reserves more).
+template <int W> __device__ __forceinline__ bool block_any(bool v, int (&flags)[W], int lane, int wave) {
+  const bool w = __any(v);
+  if (lane == 0) flags[wave] = w ? 1 : 0;
+  __syncthreads();
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < W; ++i) any = any || flags[i] != 0;
+  return any;
 }
 
 // Value of lane-1 (identity in lane 0).

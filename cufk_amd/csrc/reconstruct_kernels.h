@@ -61,6 +61,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   __shared__ R wave_total[W][12];
   __shared__ R base[12];  // first-frame rotation (row-major) and p2
   __shared__ R wave_stat[W][3];
+  __shared__ int wide_vote[W];
 
   const int steps = points - 3;
   const int64_t row = blockIdx.x;
@@ -74,10 +75,11 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   const int s0 = tid * K;
   const int count = steps - s0 < K ? steps - s0 : K;  // items of this lane (may be <= 0)
 
+  bool wide;  // some angle of the chain needs the library sin/cos
   {
     R* const dst[3] = {stage, stage + Lay::kStepRow, stage + 2 * Lay::kStepRow};
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
-    load_step_rows<Lay, 3>(dst, src, steps, tid);
+    wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
   FirstFrame<R> ff;
   if (wave == 0) {
@@ -90,31 +92,38 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
       base[11] = ff.p2.z;
     }
   }
-  __syncthreads();
+  wide = block_any<W>(wide, wide_vote, lane, wave);
 
   // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
   // translation of the lane-local prefix after item i.  Items are read from LDS as the scan
-  // reaches them, so only y stays in registers.
+  // reaches them, so only y stays in registers.  The library sin/cos is compiled into a
+  // second instance of the loop that runs only for chains with out-of-range angles.
   const int b0 = Lay::lane_step_base(tid);
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
+  auto serial = [&]<bool Checked>() {
 #pragma unroll
-  for (int i = 0; i < K; ++i) {
-    if (i < count) {
-      const R l = stage[b0 + i];
-      double s, c, S, C;
-      sin_cos_wide(stage[Lay::kStepRow + b0 + i], s, c);
-      sin_cos_wide(stage[2 * Lay::kStepRow + b0 + i], S, C);
-      step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
-      ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
-      lmin = fmin(lmin, l);
+    for (int i = 0; i < K; ++i) {
+      if (i < count) {
+        const R l = stage[b0 + i];
+        double s, c, S, C;
+        sin_cos_wide<Checked>(stage[Lay::kStepRow + b0 + i], s, c);
+        sin_cos_wide<Checked>(stage[2 * Lay::kStepRow + b0 + i], S, C);
+        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
+        lmin = fmin(lmin, l);
+      }
+      y[i][0] = static_cast<R>(q.v[0]);
+      y[i][1] = static_cast<R>(q.v[1]);
+      y[i][2] = static_cast<R>(q.v[2]);
     }
-    y[i][0] = static_cast<R>(q.v[0]);
-    y[i][1] = static_cast<R>(q.v[1]);
-    y[i][2] = static_cast<R>(q.v[2]);
-  }
+  };
+  if (wide)
+    serial.template operator()<true>();
+  else
+    serial.template operator()<false>();
 
   // lane_carry's barrier also publishes base[] and retires every read of the staged step
   // rows, which the point row below overwrites.
@@ -203,7 +212,8 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
                                             T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                             compute_t<T>* pstage, compute_t<T>* gstage,
                                             compute_t<T> (&wave_total)[Lay::kWaves][12],
-                                            compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
+                                            compute_t<T> (&wave_sum)[Lay::kWaves][6], int (&wide_vote)[Lay::kWaves],
+                                            int points) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -214,16 +224,17 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
   const int s0 = tid * K;
   const int b0 = Lay::lane_step_base(tid);
   const int o0 = Lay::lane_point_base(tid);
+  bool wide;  // some angle of the chain needs the library sin/cos
   {
     R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
-    load_step_rows<Lay, 3>(dst, src, steps, tid);
+    wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
     R* const gdst[1] = {gstage};
     const T* const gsrc[1] = {Gr};
     load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
   }
   const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-  __syncthreads();
+  wide = block_any<W>(wide, wide_vote, lane, wave);
 
   // Pass 1: lane-local scan (double); Y = sum_i y_i g_i^T and sum_i g_i.
   Rigid<double> qd = rigid_identity<double>();
@@ -231,25 +242,31 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 #pragma unroll
   for (int i = 0; i < 9; ++i) Y[i] = R(0);
   V3<R> gsum = {R(0), R(0), R(0)};
+  auto pass1 = [&]<bool Checked>() {
 #pragma unroll
-  for (int i = 0; i < K; ++i) {
-    if (s0 + i < steps) {
-      const R l = pstage[b0 + i];
-      double s, c, S, C;
-      sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
-      sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
-      step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
-      const V3<R> g = load3(&gstage[o0 + 3 * i]);
-      const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
+    for (int i = 0; i < K; ++i) {
+      if (s0 + i < steps) {
+        const R l = pstage[b0 + i];
+        double s, c, S, C;
+        sin_cos_wide<Checked>(pstage[Lay::kStepRow + b0 + i], s, c);
+        sin_cos_wide<Checked>(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+        step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
+        const V3<R> g = load3(&gstage[o0 + 3 * i]);
+        const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
 #pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        Y[3 * a + 0] += yv[a] * g.x;
-        Y[3 * a + 1] += yv[a] * g.y;
-        Y[3 * a + 2] += yv[a] * g.z;
+        for (int a = 0; a < 3; ++a) {
+          Y[3 * a + 0] += yv[a] * g.x;
+          Y[3 * a + 1] += yv[a] * g.y;
+          Y[3 * a + 2] += yv[a] * g.z;
+        }
+        gsum = gsum + g;
       }
-      gsum = gsum + g;
     }
-  }
+  };
+  if (wide)
+    pass1.template operator()<true>();
+  else
+    pass1.template operator()<false>();
 
   const Rigid<R> q = narrow_rigid<R>(qd);
   const Rigid<R> excl = lane_carry<R, W>(q, wave_total, lane, wave);
@@ -288,30 +305,36 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 
   // Pass 2: walk the lane's steps backwards; the outputs of step s replace g_{s+3} in LDS.
   V3<R> Fs = tail.f, Ms = tail.m;
+  auto pass2 = [&]<bool Checked>() {
 #pragma unroll
-  for (int i = K - 1; i >= 0; --i) {
-    if (s0 + i < steps) {
-      const V3<R> g = load3(&gstage[o0 + 3 * i]);
-      Fs = Fs + g;
-      Ms = Ms + cross(x, g);
-      const R l = pstage[b0 + i];
-      const V3<R> col0 = {Rm[0], Rm[3], Rm[6]};
-      const V3<R> col2 = {Rm[2], Rm[5], Rm[8]};
-      const V3<R> xp = x - l * col0;
-      const V3<R> tau = Ms - cross(xp, Fs);
-      const R gl = dot(col0, Fs);
-      const R ga = -dot(col2, tau);
-      double s, c, S, C;
-      sin_cos_wide(pstage[Lay::kStepRow + b0 + i], s, c);
-      sin_cos_wide(pstage[2 * Lay::kStepRow + b0 + i], S, C);
-      step_backward(Rm, static_cast<R>(s), static_cast<R>(c), static_cast<R>(S), static_cast<R>(C));
-      const R gd = dot(V3<R>{Rm[0], Rm[3], Rm[6]}, tau);
-      gstage[o0 + 3 * i] = gl;
-      gstage[o0 + 3 * i + 1] = ga;
-      gstage[o0 + 3 * i + 2] = gd;
-      x = xp;
+    for (int i = K - 1; i >= 0; --i) {
+      if (s0 + i < steps) {
+        const V3<R> g = load3(&gstage[o0 + 3 * i]);
+        Fs = Fs + g;
+        Ms = Ms + cross(x, g);
+        const R l = pstage[b0 + i];
+        const V3<R> col0 = {Rm[0], Rm[3], Rm[6]};
+        const V3<R> col2 = {Rm[2], Rm[5], Rm[8]};
+        const V3<R> xp = x - l * col0;
+        const V3<R> tau = Ms - cross(xp, Fs);
+        const R gl = dot(col0, Fs);
+        const R ga = -dot(col2, tau);
+        double s, c, S, C;
+        sin_cos_wide<Checked>(pstage[Lay::kStepRow + b0 + i], s, c);
+        sin_cos_wide<Checked>(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+        step_backward(Rm, static_cast<R>(s), static_cast<R>(c), static_cast<R>(S), static_cast<R>(C));
+        const R gd = dot(V3<R>{Rm[0], Rm[3], Rm[6]}, tau);
+        gstage[o0 + 3 * i] = gl;
+        gstage[o0 + 3 * i + 1] = ga;
+        gstage[o0 + 3 * i + 2] = gd;
+        x = xp;
+      }
     }
-  }
+  };
+  if (wide)
+    pass2.template operator()<true>();
+  else
+    pass2.template operator()<false>();
   if (tid == 0) {
     // First-frame parameters (block.cu:206-228); x2 is the origin, so M_2 = M_3.
     const V3<R> g1 = load3(&gstage[3]);
@@ -340,11 +363,13 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
   __shared__ __align__(16) R gstage[Lay::kPointRow];     // upstream gradient, then the outputs
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
+  __shared__ int wide_vote[W];
   for (int64_t row = blockIdx.x; row < batch; row += gridDim.x) {
     exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                         first_direction, initial_normal, grad_xyz + row * points * 3,
                         grad_lengths + row * (points - 1), grad_angles + row * (points - 2),
-                        grad_dihedrals + row * (points - 3), pstage, gstage, wave_total, wave_sum, points);
+                        grad_dihedrals + row * (points - 3), pstage, gstage, wave_total, wave_sum, wide_vote,
+                        points);
     __syncthreads();  // the next chain's loads overwrite the staging rows
   }
 }
@@ -477,6 +502,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
   __shared__ __align__(16) R region_b[Lay::kPointRow];
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
+  __shared__ int wide_vote[W];
   const int64_t row = blockIdx.x;
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
@@ -487,7 +513,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
   } else {
     exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                         first_direction, initial_normal, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a,
-                        region_b, wave_total, wave_sum, points);
+                        region_b, wave_total, wave_sum, wide_vote, points);
   }
 }
 

@@ -83,9 +83,11 @@ template <typename Lay, typename V, typename S> __device__ __forceinline__ V lds
 // write, so a workgroup pays one memory latency per staging phase, not one per group.
 // MaxN bounds n at compile time.  A 16-byte group never straddles a lane segment, so its
 // elements land in consecutive slots; Vec writes it with one vector LDS store (slots 16-byte
-// aligned), otherwise element by element.
-template <int NR, int MaxN, int Lanes, bool Vec, typename T, typename SlotFn>
-__device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
+// aligned), otherwise element by element.  Returns whether any element this thread staged
+// from a row in RangeRows (bit r for row r) lies beyond the polynomial range of
+// sin_cos_wide.
+template <int NR, int MaxN, int Lanes, bool Vec, unsigned RangeRows = 0, typename T, typename SlotFn>
+__device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
                                            int tid, SlotFn slot) {
   using R = compute_t<T>;
   if constexpr (Unit<T>::kElems > 1) {
@@ -107,6 +109,7 @@ __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const
 #pragma unroll
       for (int r = 0; r < NR; ++r) tail[r] = src[r][first + te];
     }
+    bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int g = tid + j * Lanes;
@@ -120,16 +123,25 @@ __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const
 #pragma unroll
             for (int e = 0; e < E; ++e) d[e] = buf[r][j][e];
           }
+          if ((RangeRows >> r) & 1u) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) wide = wide || beyond_wide_reduce(buf[r][j][e]);
+          }
         }
       }
     }
     if (te < n) {
 #pragma unroll
-      for (int r = 0; r < NR; ++r) dst[r][slot(first + te)] = tail[r];
+      for (int r = 0; r < NR; ++r) {
+        dst[r][slot(first + te)] = tail[r];
+        if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(tail[r]);
+      }
     }
+    return wide;
   } else {
     constexpr int kPer = (MaxN + Lanes - 1) / Lanes;
     R buf[NR][kPer];
+    bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int e = tid + j * Lanes;
@@ -143,16 +155,21 @@ __device__ __forceinline__ void stage_rows(compute_t<T>* const (&dst)[NR], const
       const int e = tid + j * Lanes;
       if (e < n) {
 #pragma unroll
-        for (int r = 0; r < NR; ++r) dst[r][slot(first + e)] = buf[r][j];
+        for (int r = 0; r < NR; ++r) {
+          dst[r][slot(first + e)] = buf[r][j];
+          if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(buf[r][j]);
+        }
       }
     }
+    return wide;
   }
 }
 
-// NR step rows (n <= kCap elements each) into step layouts.
-template <typename Lay, int NR, typename T>
-__device__ __forceinline__ void load_step_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int n, int tid) {
-  stage_rows<NR, Lay::kCap, Lay::kLanes, Lay::kVec, T>(dst, src, 0, n, tid, [](int s) { return Lay::step_slot(s); });
+// NR step rows (n <= kCap elements each) into step layouts; see stage_rows for RangeRows.
+template <typename Lay, int NR, unsigned RangeRows = 0, typename T>
+__device__ __forceinline__ bool load_step_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int n, int tid) {
+  return stage_rows<NR, Lay::kCap, Lay::kLanes, Lay::kVec, RangeRows, T>(dst, src, 0, n, tid,
+                                                                         [](int s) { return Lay::step_slot(s); });
 }
 
 // NR (points, 3) rows into point layouts.
@@ -163,7 +180,7 @@ __device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], 
 #pragma unroll
     for (int r = 0; r < NR; ++r) dst[r][tid] = widen(src[r][tid]);
   }
-  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, T>(dst, src, 9, 3 * points - 9, tid,
+  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, 0u, T>(dst, src, 9, 3 * points - 9, tid,
                                                            [](int e) { return Lay::point_slot(e); });
 }
 
