@@ -436,3 +436,49 @@ def test_mixed_regular_and_irregular_batch(cufk, device):
         err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
         print("per-chain rel err", err)
         assert err.max() <= 2e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_angles_beyond_the_polynomial_range(cufk, device, dtype):
+    """Angles with |x| > 65536 take the library sin/cos (the kernels switch the whole chain to
+    the checked loop).  Chain 0 is ordinary, chain 1 regular with one huge dihedral, chain 2
+    irregular (negative bond) with a huge dihedral and a huge bond angle, chain 3 a huge
+    angle near a lane boundary.  Forward, the one-launch backward and the exact backward
+    against the oracle on the same (dtype-rounded) inputs; fp32 tolerances as above, bf16
+    compared with a loose 2e-2 relative bound (it computes in float from rounded inputs)."""
+    lib = _abi()
+    B, N = 4, 300
+    d = _inputs(B, N, seed=25, anchors=True, dtype=dtype)
+    d["dihedrals"][1, 50] += 2 * math.pi * 20000.0
+    d["lengths"][2, 10] *= -1
+    d["dihedrals"][2, 123] -= 2 * math.pi * 30000.0
+    d["angles"][2, 200] += 2 * math.pi * 15000.0
+    d["angles"][3, 8] = -1.0e6
+    d = {k: _round(v, dtype) for k, v in d.items()}
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    xyz, reg = _flagged_forward(lib, L, A, D, an)
+    ref_x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    tol_x = 1e-4 if dtype == torch.float32 else 2e-2
+    err_x = np.abs(xyz.double().cpu().numpy() - ref_x).max() / max(1.0, np.abs(ref_x).max())
+    print(f"{dtype} wide-range forward: rel max err {err_x:.2e}, flags {reg.cpu().tolist()}")
+    assert err_x <= tol_x
+    if dtype == torch.float32:
+        assert reg.cpu().tolist()[:3] == [1, 1, 0]
+    p = lambda t: t.data_ptr()  # noqa: E731
+    st = torch.cuda.current_stream().cuda_stream
+    saved = [torch.empty_like(t) for t in (L, A, D)]
+    exact = [torch.empty_like(t) for t in (L, A, D)]
+    code = _CODES[dtype]
+    assert lib.cufk_reconstruct_bwd_saved(code, p(L), p(A), p(D), *map(p, an), p(xyz), p(reg), p(g), *map(p, saved), B,
+                                          N, st) == 0
+    assert lib.cufk_reconstruct_bwd(code, p(L), p(A), p(D), *map(p, an), p(g), *map(p, exact), B, N, st) == 0
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    tol = 2e-4 if dtype == torch.float32 else 5e-2
+    for name, s_, e_, r in zip(("lengths", "angles", "dihedrals"), saved, exact, ref):
+        scale = np.abs(r).max(axis=1, keepdims=True)
+        es = (np.abs(s_.double().cpu().numpy() - r) / scale).max()
+        ee = (np.abs(e_.double().cpu().numpy() - r) / scale).max()
+        print(f"{dtype} wide-range d/d{name}: saved rel {es:.2e}, exact rel {ee:.2e}")
+        assert es <= tol and ee <= tol
