@@ -97,11 +97,25 @@ __device__ __forceinline__ bool beyond_wide_reduce(float x) { return fabsf(x) > 
 __device__ __forceinline__ bool beyond_wide_reduce(double) { return false; }
 
 // Unit (sin, cos) from a raw pair in double (torsion.cu:119-141 clamps rs^2 + rc^2 at 1e-16).
+// For float pairs 1/sqrt comes from the float reciprocal square root refined by one Newton
+// step in double (relative error ~1e-14, against a 20-odd instruction double sqrt and
+// divide); beyond the float range of rs^2 + rc^2 and for double pairs it is 1/sqrt in double.
 template <typename R> __device__ __forceinline__ void pair_unit(R rs, R rc, double& S, double& C) {
   const double a = rs, b = rc;
   const double n2 = a * a + b * b;
   const double eps2 = static_cast<double>(1.0e-8f * 1.0e-8f);
-  const double rinv = 1.0 / sqrt(n2 < eps2 ? eps2 : n2);
+  const double m = n2 < eps2 ? eps2 : n2;
+  double rinv;
+  if constexpr (sizeof(R) == 4) {
+    if (m < 1.0e38) {
+      const double r0 = __builtin_amdgcn_rsqf(static_cast<float>(m));
+      rinv = r0 * fma(-0.5 * m, r0 * r0, 1.5);
+    } else {
+      rinv = 1.0 / sqrt(m);
+    }
+  } else {
+    rinv = 1.0 / sqrt(m);
+  }
   S = a * rinv;
   C = b * rinv;
 }

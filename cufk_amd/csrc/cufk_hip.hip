@@ -44,6 +44,15 @@ template <typename Fn> int with_torsion_plan(int steps, Fn&& fn) {
   return fn.template operator()<3, 12>();
 }
 
+// Torsion backward plans: three steps per lane (no LDS staging, see torsion_backward_kernel).
+template <typename Fn> int with_torsion_bwd_plan(int steps, Fn&& fn) {
+  if (steps <= 192) return fn.template operator()<1, 3>();
+  if (steps <= 384) return fn.template operator()<2, 3>();
+  if (steps <= 768) return fn.template operator()<4, 3>();
+  if (steps <= 1536) return fn.template operator()<8, 3>();
+  return fn.template operator()<11, 3>();
+}
+
 // HIP's grid x extent counts work-items in 32 bits: launch one-chain-per-workgroup kernels
 // in chunks of at most UINT32_MAX / threads workgroups.
 template <typename Fn> int launch_chunks(int64_t batch, int threads, Fn&& fn) {
@@ -114,7 +123,7 @@ int torsion_fwd_typed(const T* raw, int64_t rs, const TorsionArgs& c, T* xyz, in
 template <typename T>
 int torsion_bwd_typed(const T* raw, int64_t rs, const T* xyz, const T* g, T* graw, int64_t gs, const TorsionArgs& c,
                       int64_t B, int N, hipStream_t st) {
-  return with_torsion_plan(N - 3, [&]<int W, int K>() {
+  return with_torsion_bwd_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((torsion_backward_kernel<T, W, K>), dim3(n), dim3(64 * W), 0, st, raw + off * rs, rs,
                          xyz + off * N * 3, g + off * N * 3, graw + off * gs, gs, c, N);

@@ -184,6 +184,55 @@ __device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], 
                                                            [](int e) { return Lay::point_slot(e); });
 }
 
+// One lane's run of n <= N consecutive elements between global memory and registers, in
+// 16-byte vectors where the run allows (dword alignment suffices for float and double rows)
+// and element by element for the remainder and for float16/bfloat16.
+template <int N, typename T>
+__device__ __forceinline__ void load_run(const T* __restrict__ src, int n, compute_t<T> (&dst)[N]) {
+  constexpr int E = Unit<T>::kElems;
+  if constexpr (E > 1) {
+#pragma unroll
+    for (int j = 0; j + E <= N; j += E) {
+      if (j + E <= n) {
+        const typename Unit<T>::Local v = *reinterpret_cast<const typename Unit<T>::Global*>(src + j);
+#pragma unroll
+        for (int e = 0; e < E; ++e) dst[j + e] = v[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (j + e < n) dst[j + e] = src[j + e];
+      }
+    }
+  }
+  constexpr int kTail = E > 1 ? (N / E) * E : 0;  // first element not covered by a vector
+#pragma unroll
+  for (int j = kTail; j < N; ++j)
+    if (j < n) dst[j] = widen(src[j]);
+}
+template <int N, typename T>
+__device__ __forceinline__ void store_run(T* __restrict__ dst, int n, const compute_t<T> (&src)[N]) {
+  constexpr int E = Unit<T>::kElems;
+  if constexpr (E > 1) {
+#pragma unroll
+    for (int j = 0; j + E <= N; j += E) {
+      if (j + E <= n) {
+        typename Unit<T>::Local v;
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = src[j + e];
+        *reinterpret_cast<typename Unit<T>::Global*>(dst + j) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (j + e < n) dst[j + e] = src[j + e];
+      }
+    }
+  }
+  constexpr int kTail = E > 1 ? (N / E) * E : 0;
+#pragma unroll
+  for (int j = kTail; j < N; ++j)
+    if (j < n) dst[j] = narrow<T>(src[j]);
+}
+
 // dst[s] = src[step_slot(s)] for s in [0, n).
 template <typename Lay, typename T>
 __device__ __forceinline__ void store_step_row(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int n, int tid) {

@@ -161,20 +161,19 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
 // Backward (torsion.cu:297-381) over the saved positions:
 //   dphi_k = (1/l_{(k+1)%3}) (x_{k+2} - x_{k+1}) . (M_{k+3} - x_{k+2} x F_{k+3}),
 //   raw grad = dphi (rc, -rs) / max(rs^2 + rc^2, 1e-16) (torsion.cu:173-182),
-// with positions relative to x2 (the moments are translation invariant).
+// with positions relative to x2 (the moments are translation invariant).  No LDS staging:
+// each lane moves its own contiguous runs (points s0 .. s0+K+2, their gradients, its raw
+// pairs and its raw-pair gradients) straight between HBM and registers; only the wave sums
+// of the suffix scan go through LDS.  With K = 3 (the smallest multiple of the phase period)
+// a workgroup per chain holds up to eight waves per SIMD, where staging whole rows through
+// LDS held one or two.
 template <typename T, int W, int K>
 __global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __restrict__ raw_pairs, int64_t raw_stride,
                                                                   const T* __restrict__ xyz, const T* __restrict__ grad_xyz,
                                                                   T* __restrict__ grad_raw, int64_t grad_raw_stride,
                                                                   TorsionArgs cst, int points) {
-  static_assert(K % 12 == 0, "torsion plans keep phases lane-invariant and segments 16-byte aligned");
+  static_assert(K % 3 == 0, "torsion plans keep phases lane-invariant");
   using R = compute_t<T>;
-  using Lay = Layout<W, K>;
-  __shared__ __align__(16) R xs[Lay::kPointRow];
-  __shared__ __align__(16) R gs[Lay::kPointRow];  // upstream gradient, then the raw-pair gradients
-  // float64 rows would overflow LDS at the largest plan; those read raw pairs from global.
-  constexpr bool kStageRaw = sizeof(R) == 4;
-  __shared__ __align__(16) R rstage[kStageRaw ? 2 * Lay::kStepRow : 4];
   __shared__ R wave_sum[W][6];
 
   const int steps = points - 3;
@@ -186,70 +185,48 @@ __global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __res
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-
-  if constexpr (kStageRaw) load_pair_rows<Lay>(rstage, rstage + Lay::kStepRow, raw, steps, tid);
-  {
-    R* const dst[2] = {xs, gs};
-    const T* const src[2] = {Xr, Gr};
-    load_point_rows<Lay, 2>(dst, src, points, tid);
-  }
-  __syncthreads();
-
-  const V3<R> c = load3(&xs[6]);
-  auto pos = [&](int p) { return load3(&xs[Lay::point_slot(3 * p)]) - c; };
   const int s0 = tid * K;
-  const int o0 = Lay::lane_point_base(tid);
-  const int b0 = Lay::lane_step_base(tid);
-  const int last = (steps - s0 < K ? steps - s0 : K) - 1;
+  const int count = steps - s0 < K ? (steps - s0 > 0 ? steps - s0 : 0) : K;
+  const int last = count - 1;
+
+  R xr[3 * K + 9], gr[3 * K], pr[2 * K];
+  load_run<3 * K + 9>(Xr + 3 * s0, count > 0 ? 3 * (count + 3) : 0, xr);
+  load_run<3 * K>(Gr + 9 + 3 * s0, 3 * count, gr);
+  load_run<2 * K>(raw + 2 * s0, 2 * count, pr);
+  const V3<R> c = {widen(Xr[6]), widen(Xr[7]), widen(Xr[8])};
+  auto pos = [&](int j) { return V3<R>{xr[3 * j], xr[3 * j + 1], xr[3 * j + 2]} - c; };
 
   ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (i <= last) {
-      const V3<R> x = load3(&xs[o0 + 3 * i]) - c;
-      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      const V3<R> g = {gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]};
       lane_sum.f = lane_sum.f + g;
-      lane_sum.m = lane_sum.m + cross(x, g);
+      lane_sum.m = lane_sum.m + cross(pos(i + 3), g);
     }
   }
   const ForceMoment<R> tail = lane_suffix<R, W>(lane_sum, wave_sum, lane, wave);
 
   V3<R> F = tail.f, M = tail.m;
-  V3<R> xa, xb, xc;  // x_p, x_{p-1}, x_{p-2}
-  if (last >= 0) {
-    const int p = 3 + s0 + last;
-    xa = pos(p);
-    xb = pos(p - 1);
-    xc = pos(p - 2);
-  }
   const R eps2 = static_cast<R>(1.0e-8f * 1.0e-8f);
+  R go[2 * K];
 #pragma unroll
   for (int i = K - 1; i >= 0; --i) {
+    go[2 * i] = go[2 * i + 1] = R(0);
     if (i <= last) {
-      const int p = 3 + s0 + i;
-      const V3<R> g = load3(&gs[o0 + 3 * i]);
+      const V3<R> xa = pos(i + 3), xb = pos(i + 2), xc = pos(i + 1);
+      const V3<R> g = {gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]};
       F = F + g;
       M = M + cross(xa, g);
       const R dphi = static_cast<R>(cst.inv_length[(i + 1) % 3]) * dot(xb - xc, M - cross(xb, F));
-      R rs, rc;
-      if constexpr (kStageRaw) {
-        rs = rstage[b0 + i];
-        rc = rstage[Lay::kStepRow + b0 + i];
-      } else {
-        rs = widen(raw[2 * (p - 3)]);
-        rc = widen(raw[2 * (p - 3) + 1]);
-      }
+      const R rs = pr[2 * i], rc = pr[2 * i + 1];
       const R n2 = rs * rs + rc * rc;
       const R scale = dphi / (n2 < eps2 ? eps2 : n2);
-      gs[o0 + 3 * i] = rc * scale;
-      gs[o0 + 3 * i + 1] = -rs * scale;
-      xa = xb;
-      xb = xc;
-      xc = pos(p - 3);
+      go[2 * i] = rc * scale;
+      go[2 * i + 1] = -rs * scale;
     }
   }
-  __syncthreads();
-  store_interleaved_pairs<Lay>(graw, gs, steps, tid);
+  store_run<2 * K>(graw + 2 * s0, 2 * count, go);
 }
 
 }  // namespace cufk_amd

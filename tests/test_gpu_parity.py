@@ -196,7 +196,7 @@ def test_backward_fp32_tolerance(cufk, device, N):
 # ----------------------------------------------------------------- torsion
 
 
-@pytest.mark.parametrize("N", [4, 5, 6, 7, 100, 387, 388, 771, 772, 1539, 1540, 2051])
+@pytest.mark.parametrize("N", [4, 5, 6, 7, 100, 195, 196, 387, 388, 771, 772, 1539, 1540, 2051])
 def test_torsion_fp64_matches_oracle(cufk, device, N):
     rng = np.random.default_rng(N)
     B = 3
@@ -247,6 +247,46 @@ def test_torsion_fp32_tolerance(cufk, device):
     print(f"torsion fp32 N={N}: rms {rms:.3e}, max {np.abs(diff).max():.3e}, grad rel {gerr:.3e}")
     assert rms <= 1e-5 and np.abs(diff).max() <= 1e-4
     assert gerr <= 2e-4
+
+
+@pytest.mark.parametrize("N", [4, 5, 100, 195, 196, 388, 772, 1540, 2051])
+def test_torsion_fp32_gradients_across_plans(cufk, device, N):
+    """fp32 raw-pair gradients at every backward plan size (3 steps per lane, 1-11 waves)."""
+    rng = np.random.default_rng(900 + N)
+    B = 3
+    raw = _round(rng.normal(size=(B, 2 * (N - 3))), torch.float32)
+    g = _round(rng.normal(size=(B, N, 3)), torch.float32)
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    r = _dev(raw, torch.float32, device, True)
+    xyz = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)(r)
+    (graw,) = torch.autograd.grad(xyz, (r,), _dev(g, torch.float32, device))
+    ref_g = o.torsion_backward(raw, o.torsion_forward(raw, consts), g, consts)
+    gerr = np.abs(graw.double().cpu().numpy() - ref_g).max() / np.abs(ref_g).max()
+    print(f"torsion fp32 N={N}: grad rel {gerr:.3e}")
+    assert gerr <= 2e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_torsion_low_precision_reported(cufk, device, dtype):
+    """Half-precision torsion: computed in float from the rounded inputs; errors against the
+    float64 oracle on the same inputs are reported, with only a loose sanity bound.  The
+    backward works from the saved half-precision positions (as the reference's does), whose
+    rounding (about 0.02 nm at chain scale in bfloat16) dominates the gradient error."""
+    rng = np.random.default_rng(31)
+    B, N = 4, 300
+    raw = _round(rng.normal(size=(B, 2 * (N - 3))), dtype)
+    g = _round(rng.normal(size=(B, N, 3)), dtype)
+    consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    r = _dev(raw, dtype, device, True)
+    xyz = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)(r)
+    (graw,) = torch.autograd.grad(xyz, (r,), _dev(g, dtype, device))
+    ref = o.torsion_forward(raw, consts)
+    ref_g = o.torsion_backward(raw, ref, g, consts)
+    err = np.abs(xyz.detach().double().cpu().numpy() - ref).max() / np.abs(ref).max()
+    gerr = np.abs(graw.double().cpu().numpy() - ref_g).max() / np.abs(ref_g).max()
+    print(f"torsion {dtype} N={N}: xyz rel {err:.3e}, grad rel {gerr:.3e}")
+    assert torch.isfinite(xyz).all() and torch.isfinite(graw).all()
+    assert err <= 5e-2 and gerr <= 0.5
 
 
 def test_torsion_strided_rows_keep_grad_strides(cufk, device):
