@@ -79,17 +79,16 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
   });
 }
 
-// Exact backward for every chain; the kernel strides over chains, so any grid size covers
-// the batch.
+// Exact backward for every chain.
 template <typename T>
 int reconstruct_bwd_exact_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* g,
                                 T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
-    const int64_t cap = 65536;
-    const unsigned grid = static_cast<unsigned>(B < cap ? B : cap);
-    hipLaunchKernelGGL((reconstruct_backward_exact_kernel<T, W, K, kScanPad>), dim3(grid), dim3(64 * W), 0, st, L, A, D, p0, fd,
-                       n0, g, gL, gA, gD, N, static_cast<int>(B));
-    return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_backward_exact_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, g + off * N * 3,
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+    });
   });
 }
 

@@ -350,13 +350,13 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
   store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gstage, steps, tid);
 }
 
-// Exact backward for every chain; the workgroups stride over the batch.
+// Exact backward, one workgroup per chain.
 template <typename T, int W, int K, int Pad = 4>
 __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points, int batch) {
+    T* __restrict__ grad_dihedrals, int points) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   __shared__ __align__(16) R pstage[3 * Lay::kStepRow];  // parameters
@@ -364,14 +364,11 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
   __shared__ int wide_vote[W];
-  for (int64_t row = blockIdx.x; row < batch; row += gridDim.x) {
-    exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
-                        first_direction, initial_normal, grad_xyz + row * points * 3,
-                        grad_lengths + row * (points - 1), grad_angles + row * (points - 2),
-                        grad_dihedrals + row * (points - 3), pstage, gstage, wave_total, wave_sum, wide_vote,
-                        points);
-    __syncthreads();  // the next chain's loads overwrite the staging rows
-  }
+  const int64_t row = blockIdx.x;
+  exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
+                      first_direction, initial_normal, grad_xyz + row * points * 3, grad_lengths + row * (points - 1),
+                      grad_angles + row * (points - 2), grad_dihedrals + row * (points - 3), pstage, gstage, wave_total,
+                      wave_sum, wide_vote, points);
 }
 
 // ============================================================================ position-based backward
