@@ -89,6 +89,59 @@ __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
     if (fabsf(xf) > kWideReduceMax) sincos(x, &s, &c);
   }
 }
+// sin and cos of a float argument from a 16-entry table and short polynomials, for the hot
+// loop of the forward: k = rint(8x/pi), r = x - k pi/8 (two-part Cody-Waite) with |r| <= pi/16,
+//   sin r = r + r u (s1 + s2 u + s3 u^2),  cos r = 1 + u (c1 + c2 u + c3 u^2 + c4 u^3),  u = r^2
+// (Chebyshev fits: |error| < 4e-14 and < 2e-16), then
+//   sin x = T_s[k] cos r + T_c[k] sin r,  cos x = T_c[k] cos r - T_s[k] sin r
+// with (T_s, T_c)[j] = (sin, cos)(j pi/8) held in LDS (sin_cos_table_init).  No quadrant
+// selects; about 22 VALU issues against 30 for sin_cos_wide.  Same Checked convention.
+struct SinCosEntry {
+  double s, c;
+};
+constexpr int kSinCosTable = 16;
+__device__ __forceinline__ void sin_cos_table_init(SinCosEntry* table, int tid) {
+  constexpr double kTable[kSinCosTable][2] = {
+    {0.0, 1.0},
+    {0.3826834323650898, 0.9238795325112867},
+    {0.7071067811865476, 0.7071067811865476},
+    {0.9238795325112867, 0.3826834323650898},
+    {1.0, 0.0},
+    {0.9238795325112867, -0.3826834323650898},
+    {0.7071067811865476, -0.7071067811865476},
+    {0.3826834323650898, -0.9238795325112867},
+    {0.0, -1.0},
+    {-0.3826834323650898, -0.9238795325112867},
+    {-0.7071067811865476, -0.7071067811865476},
+    {-0.9238795325112867, -0.3826834323650898},
+    {-1.0, 0.0},
+    {-0.9238795325112867, 0.3826834323650898},
+    {-0.7071067811865476, 0.7071067811865476},
+    {-0.3826834323650898, 0.9238795325112867}};
+  if (tid < kSinCosTable) table[tid] = SinCosEntry{kTable[tid][0], kTable[tid][1]};
+}
+template <bool Checked = true>
+__device__ __forceinline__ void sin_cos_tab(float xf, const SinCosEntry* table, double& s, double& c) {
+  const double x = xf;
+  const double k = __builtin_rint(x * 2.5464790894703255);
+  double r = fma(-k, 0.39269908169872414, x);
+  r = fma(-k, 1.5308084989341915e-17, r);
+  const double u = r * r;
+  double ps = lin_sk(u, -0.00019825339804578352, 0.008333331030517558);
+  ps = fma_sk(ps, u, -0.1666666666617345);
+  const double sr = fma(r * u, ps, r);
+  double pc = lin_sk(u, 2.478034740778822e-05, -0.0013888883771620158);
+  pc = fma_sk(pc, u, 0.041666666662721126);
+  pc = fma_sk(pc, u, -0.4999999999999952);
+  const double cr = fma_sk(u, pc, 1.0);
+  const SinCosEntry t = table[static_cast<int>(k) & (kSinCosTable - 1)];
+  s = fma(t.s, cr, t.c * sr);
+  c = fma(t.c, cr, -(t.s * sr));
+  if constexpr (Checked) {
+    if (fabsf(xf) > kWideReduceMax) sincos(x, &s, &c);
+  }
+}
+
 template <bool Checked = true>
 __device__ __forceinline__ void sin_cos_wide(double x, double& s, double& c) { sincos(x, &s, &c); }
 

@@ -62,6 +62,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   __shared__ R base[12];  // first-frame rotation (row-major) and p2
   __shared__ R wave_stat[W][3];
   __shared__ int wide_vote[W];
+  __shared__ SinCosEntry sc_table[kSinCosTable];
 
   const int steps = points - 3;
   const int64_t row = blockIdx.x;
@@ -81,6 +82,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
+  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid);
   FirstFrame<R> ff;
   if (wave == 0) {
     ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
@@ -109,8 +111,13 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
       if (i < count) {
         const R l = stage[b0 + i];
         double s, c, S, C;
-        sin_cos_wide<Checked>(stage[Lay::kStepRow + b0 + i], s, c);
-        sin_cos_wide<Checked>(stage[2 * Lay::kStepRow + b0 + i], S, C);
+        if constexpr (sizeof(R) == 4) {
+          sin_cos_tab<Checked>(stage[Lay::kStepRow + b0 + i], sc_table, s, c);
+          sin_cos_tab<Checked>(stage[2 * Lay::kStepRow + b0 + i], sc_table, S, C);
+        } else {
+          sin_cos_wide<Checked>(stage[Lay::kStepRow + b0 + i], s, c);
+          sin_cos_wide<Checked>(stage[2 * Lay::kStepRow + b0 + i], S, C);
+        }
         step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
         ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
         lmin = fmin(lmin, l);
