@@ -79,13 +79,14 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
   });
 }
 
-// Exact backward for every chain.
+// Backward without a saved output: the forward scan is rerun per chain, then the
+// position-based adjoint (or the exact one for irregular chains).
 template <typename T>
-int reconstruct_bwd_exact_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* g,
-                                T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
+                                    const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_exact_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+      hipLaunchKernelGGL((reconstruct_backward_recompute_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, g + off * N * 3,
                          gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
     });
@@ -209,10 +210,10 @@ int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, con
   const int N = static_cast<int>(points);
   auto st = static_cast<hipStream_t>(stream);
   return dispatch(dtype, [&]<typename T>() {
-    return reconstruct_bwd_exact_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
-                                          cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
-                                          mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N,
-                                          st);
+    return reconstruct_bwd_recompute_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                              cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
+                                              mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N,
+                                              st);
   });
 }
 
@@ -236,11 +237,12 @@ int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angle
                                             cp<T>(grad_xyz), mp<T>(grad_lengths), mp<T>(grad_angles),
                                             mp<T>(grad_dihedrals), batch, N, st);
     } else {
-      // float16 / bfloat16 chains are never flagged regular.
-      return reconstruct_bwd_exact_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
-                                            cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
-                                            mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N,
-                                            st);
+      // float16 / bfloat16 outputs are too coarse for the position-based adjoint; the
+      // positions are recomputed in float instead.
+      return reconstruct_bwd_recompute_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                                cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
+                                                mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch,
+                                                N, st);
     }
   });
 }

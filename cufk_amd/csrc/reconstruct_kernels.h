@@ -2,10 +2,13 @@
 //
 // One workgroup of W wave64s per chain; lane t owns steps [tK, tK+K) (point s+3 for step s).
 //   reconstruct_forward_kernel     block_forward_kernel (block.cu:157-204)
-//   reconstruct_backward_exact     block_backward_kernel (block.cu:230-313): recomputes the frames
-//   reconstruct_backward_saved     the world-frame force/moment adjoint over the saved positions
-//                                  (the form torsion.cu:204-217 uses) for chains the forward
-//                                  marked regular, the exact recompute for the others
+//   reconstruct_backward_saved     block_backward_kernel (block.cu:230-313) given the forward's
+//                                  output: the world-frame force/moment adjoint over the saved
+//                                  positions (the form torsion.cu:204-217 uses) for chains the
+//                                  forward marked regular, the exact recompute for the others
+//   reconstruct_backward_recompute block_backward_kernel without a saved output: the forward
+//                                  scan rerun in registers, then the same adjoint over those
+//                                  positions (exact recompute for irregular chains)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -357,27 +360,6 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
   store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gstage, steps, tid);
 }
 
-// Exact backward, one workgroup per chain.
-template <typename T, int W, int K, int Pad = 4>
-__global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
-    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
-    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
-    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points) {
-  using R = compute_t<T>;
-  using Lay = Layout<W, K, Pad>;
-  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];  // parameters
-  __shared__ __align__(16) R gstage[Lay::kPointRow];     // upstream gradient, then the outputs
-  __shared__ R wave_total[W][12];
-  __shared__ R wave_sum[W][6];
-  __shared__ int wide_vote[W];
-  const int64_t row = blockIdx.x;
-  exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
-                      first_direction, initial_normal, grad_xyz + row * points * 3, grad_lengths + row * (points - 1),
-                      grad_angles + row * (points - 2), grad_dihedrals + row * (points - 3), pstage, gstage, wave_total,
-                      wave_sum, wide_vote, points);
-}
-
 // ============================================================================ position-based backward
 
 // Position-based adjoint for one chain the forward marked regular:
@@ -388,11 +370,12 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_exact_kernel(
 // [tK, tK+K).  Rows are staged through LDS (xs, gs: one point row each); each lane copies its
 // points [tK, tK+K+3) and gradients into registers, and its outputs replace its gradients in
 // LDS for a coalesced store.
+// The adjoint above once positions (xs) and gradients (gs) sit in LDS point rows, visible to
+// the whole workgroup.
 template <typename T, typename Lay>
-__device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T* __restrict__ Gr,
-                                               T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
-                                               compute_t<T>* xs, compute_t<T>* gs,
-                                               compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
+__device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
+                                                 compute_t<T>* xs, compute_t<T>* gs,
+                                                 compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -408,10 +391,6 @@ __device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T
   R xr[3 * K + 9], gr[3 * K];
   V3<R> c;
   {
-    R* const dst[2] = {xs, gs};
-    const T* const src[2] = {Xr, Gr};
-    load_point_rows<Lay, 2>(dst, src, points, tid);
-    __syncthreads();
     c = load3(&xs[6]);
     const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
@@ -487,6 +466,176 @@ __device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T
     __syncthreads();
     store_interleaved_rows<Lay>(gLr + 2, gAr + 1, gDr, gs, steps, tid);
   }
+}
+
+template <typename T, typename Lay>
+__device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T* __restrict__ Gr,
+                                               T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
+                                               compute_t<T>* xs, compute_t<T>* gs,
+                                               compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
+  {
+    compute_t<T>* const dst[2] = {xs, gs};
+    const T* const src[2] = {Xr, Gr};
+    load_point_rows<Lay, 2>(dst, src, points, threadIdx.x);
+  }
+  __syncthreads();
+  position_adjoint<T, Lay>(gLr, gAr, gDr, xs, gs, wave_sum, points);
+}
+
+// ============================================================================ recompute backward
+
+// Backward without a saved output: the forward scan is rerun in registers (double lane-serial,
+// float cross-lane), giving every lane its points relative to x2 in the compute precision;
+// chains that pass the regularity test on those positions (FastPath<compute type>) take the
+// position-based adjoint over them, the others exact_chain.  For float16/bfloat16 chains this
+// replaces the exact recompute, whose reverse walk costs about twice the forward, and it needs
+// no float copy of the half-precision output.  pstage: 3 step rows (then the positions),
+// gstage: the gradient row.
+template <typename T, typename Lay>
+__device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
+                                                const T* __restrict__ Dr, const T* __restrict__ p0,
+                                                const T* __restrict__ first_direction,
+                                                const T* __restrict__ initial_normal, const T* __restrict__ Gr,
+                                                T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
+                                                compute_t<T>* pstage, compute_t<T>* gstage,
+                                                compute_t<T> (&wave_total)[Lay::kWaves][12],
+                                                compute_t<T> (&wave_sum)[Lay::kWaves][6],
+                                                compute_t<T> (&wave_stat)[Lay::kWaves][3], int (&wide_vote)[Lay::kWaves],
+                                                int points) {
+  using R = compute_t<T>;
+  using Fast = FastPath<R>;
+  constexpr int W = Lay::kWaves;
+  constexpr int K = Lay::kItems;
+  const int steps = points - 3;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int s0 = tid * K;
+  const int count = steps - s0 < K ? steps - s0 : K;
+  const int b0 = Lay::lane_step_base(tid);
+  bool wide;
+  {
+    R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
+    const T* const src[3] = {Lr + 2, Ar + 1, Dr};
+    wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
+    R* const gdst[1] = {gstage};
+    const T* const gsrc[1] = {Gr};
+    load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
+  }
+  const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+  wide = block_any<W>(wide, wide_vote, lane, wave);
+
+  Rigid<double> q = rigid_identity<double>();
+  R y[K][3];
+  bool ok = true;
+  R lmin = R(1.0e30);
+  auto serial = [&]<bool Checked>() {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if (i < count) {
+        const R l = pstage[b0 + i];
+        double s, c, S, C;
+        sin_cos_wide<Checked>(pstage[Lay::kStepRow + b0 + i], s, c);
+        sin_cos_wide<Checked>(pstage[2 * Lay::kStepRow + b0 + i], S, C);
+        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        ok = ok && l > R(0) && s >= Fast::kSinMin;
+        lmin = fmin(lmin, l);
+      }
+      y[i][0] = static_cast<R>(q.v[0]);
+      y[i][1] = static_cast<R>(q.v[1]);
+      y[i][2] = static_cast<R>(q.v[2]);
+    }
+  };
+  if (wide)
+    serial.template operator()<true>();
+  else
+    serial.template operator()<false>();
+  const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
+
+  // World frame at the lane start, origin at x2.
+  R R0[9];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      R0[3 * r + c] = ff.frame[3 * r] * excl.m[c] + ff.frame[3 * r + 1] * excl.m[3 + c] + ff.frame[3 * r + 2] * excl.m[6 + c];
+  }
+  const V3<R> X0 = rot_apply(ff.frame, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+  V3<R> x[K];
+  R xmax = R(0);
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    x[i] = X0 + rot_apply(R0, V3<R>{y[i][0], y[i][1], y[i][2]});
+    if (i < count) xmax = abs_max3(xmax, x[i]);
+  }
+  {
+    const bool wave_ok = __all(ok);
+    const R wmin = wave_min(lmin);
+    const R wmax = wave_max(xmax);
+    if (lane == 0) {
+      wave_stat[wave][0] = wave_ok ? R(1) : R(0);
+      wave_stat[wave][1] = wmin;
+      wave_stat[wave][2] = wmax;
+    }
+  }
+  __syncthreads();  // also retires every read of the step rows, which the positions replace
+  bool regular = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= static_cast<R>(Fast::kSinMin);
+  {
+    R m = fmin(ff.L0, ff.L1);
+    R xm = abs_max3(abs_max3(R(0), ff.p0 - ff.p2), ff.p1 - ff.p2);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      regular = regular && wave_stat[w][0] != R(0);
+      m = fmin(m, wave_stat[w][1]);
+      xm = fmax(xm, wave_stat[w][2]);
+    }
+    regular = regular && xm <= static_cast<R>(Fast::kScale) * m;
+  }
+  if (regular) {
+    const int o0 = Lay::lane_point_base(tid);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if (i < count) {
+        pstage[o0 + 3 * i] = x[i].x;
+        pstage[o0 + 3 * i + 1] = x[i].y;
+        pstage[o0 + 3 * i + 2] = x[i].z;
+      }
+    }
+    if (tid == 0) {
+      const V3<R> a = ff.p0 - ff.p2, b = ff.p1 - ff.p2;
+      pstage[0] = a.x; pstage[1] = a.y; pstage[2] = a.z;
+      pstage[3] = b.x; pstage[4] = b.y; pstage[5] = b.z;
+      pstage[6] = R(0); pstage[7] = R(0); pstage[8] = R(0);
+    }
+    __syncthreads();
+    position_adjoint<T, Lay>(gLr, gAr, gDr, pstage, gstage, wave_sum, points);
+  } else {
+    exact_chain<T, Lay>(Lr, Ar, Dr, p0, first_direction, initial_normal, Gr, gLr, gAr, gDr, pstage, gstage, wave_total,
+                        wave_sum, wide_vote, points);
+  }
+}
+
+// Backward without a saved output, one workgroup per chain.
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_backward_recompute_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
+    T* __restrict__ grad_dihedrals, int points) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K, Pad>;
+  constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R region_a[kA];
+  __shared__ __align__(16) R region_b[Lay::kPointRow];
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
+  __shared__ R wave_stat[W][3];
+  __shared__ int wide_vote[W];
+  const int64_t row = blockIdx.x;
+  recompute_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
+                          first_direction, initial_normal, grad_xyz + row * points * 3, grad_lengths + row * (points - 1),
+                          grad_angles + row * (points - 2), grad_dihedrals + row * (points - 3), region_a, region_b,
+                          wave_total, wave_sum, wave_stat, wide_vote, points);
 }
 
 // Backward given the forward's own output: one workgroup per chain, the position-based

@@ -16,6 +16,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <type_traits>
 
 #include "chain_ops.h"
@@ -50,7 +51,7 @@ template <int W, int K, int Pad = 4> struct Layout {
 };
 
 // 16-byte global access unit for T: 4 floats or 2 doubles (dword-aligned rows suffice);
-// float16/bfloat16 rows are only 2-byte aligned and move one element at a time.
+// float16/bfloat16 rows are only 2-byte aligned and move in windows (below).
 template <typename T> struct Unit {
   static constexpr int kElems = 1;
 };
@@ -64,6 +65,42 @@ template <> struct Unit<double> {
   typedef f64x2u Global;
   typedef f64x2 Local;
 };
+
+// float16/bfloat16 rows in 16-byte windows aligned down from the row start: window g covers
+// the row's elements 8g - lead .. 8g - lead + 7, lead being the row start's element offset in
+// its 16-byte block.  A load may read bytes of the first and last window that lie outside the
+// row; they share a 16-byte block, hence a page, with bytes of the row, and are discarded.
+// Stores write whole windows only inside the row and single elements at its two ends, so
+// rows written by other workgroups are never touched.
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+template <typename T> __device__ __forceinline__ int window_lead(const T* p) {
+  static_assert(sizeof(T) == 2, "windows are for 2-byte elements");
+  return static_cast<int>((reinterpret_cast<uintptr_t>(p) >> 1) & 7);
+}
+template <typename T> __device__ __forceinline__ int window_count(int n, int lead) { return n > 0 ? (n + lead + 7) >> 3 : 0; }
+
+// dst[e] = val(e) for e in [0, n), by the Lanes threads of a workgroup.
+template <int Lanes, typename T, typename ValFn>
+__device__ __forceinline__ void store_windows(T* __restrict__ dst, int n, int tid, ValFn val) {
+  const int lead = window_lead(dst);
+  const int windows = window_count<T>(n, lead);
+  for (int g = tid; g < windows; g += Lanes) {
+    const int e0 = 8 * g - lead;
+    if (e0 >= 0 && e0 + 8 <= n) {
+      u16x8 v;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const T x = val(e0 + k);
+        v[k] = __builtin_bit_cast(unsigned short, x);
+      }
+      *reinterpret_cast<u16x8*>(dst + e0) = v;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (e0 + k >= 0 && e0 + k < n) dst[e0 + k] = val(e0 + k);
+    }
+  }
+}
 
 // A 16-byte group of consecutive LDS slots: one vector read when the layout keeps lane runs
 // 16-byte aligned, element reads otherwise.
@@ -135,6 +172,44 @@ __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const
       for (int r = 0; r < NR; ++r) {
         dst[r][slot(first + te)] = tail[r];
         if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(tail[r]);
+      }
+    }
+    return wide;
+  } else if constexpr (sizeof(T) == 2) {
+    constexpr int kPer = (MaxN / 8 + 1 + Lanes - 1) / Lanes;  // a misaligned row spans one more window
+    u16x8 buf[NR][kPer];
+    int lead[NR], windows[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      lead[r] = window_lead(src[r] + first);
+      windows[r] = window_count<T>(n, lead[r]);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lanes;
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        if (g < windows[r]) buf[r][j] = *reinterpret_cast<const u16x8*>(src[r] + first - lead[r] + 8 * g);
+    }
+    bool wide = false;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int g = tid + j * Lanes;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (g < windows[r]) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int e = 8 * g - lead[r] + k;
+            if (e >= 0 && e < n) {
+              // Through a scalar: a bit cast of the vector element itself reads element 0.
+              const unsigned short bits = buf[r][j][k];
+              const R v = widen(__builtin_bit_cast(T, bits));
+              dst[r][slot(first + e)] = v;
+              if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(v);
+            }
+          }
+        }
       }
     }
     return wide;
@@ -268,7 +343,7 @@ __device__ __forceinline__ void store_point_row(T* __restrict__ dst, const compu
       *reinterpret_cast<f64x2u*>(dst + 9 + 2 * g) = lds_vec<Lay, f64x2>(src + Lay::point_slot(9 + 2 * g));
     if ((n & 1) && tid == 0) dst[9 + n - 1] = src[Lay::point_slot(9 + n - 1)];
   } else {
-    for (int e = tid; e < n; e += Lay::kLanes) dst[9 + e] = narrow<T>(src[Lay::point_slot(9 + e)]);
+    store_windows<Lay::kLanes>(dst + 9, n, tid, [&](int e) { return narrow<T>(src[Lay::point_slot(9 + e)]); });
   }
 }
 
@@ -296,6 +371,10 @@ __device__ __forceinline__ void store_interleaved_rows(T* __restrict__ a, T* __r
       b[s] = p[1];
       c[s] = p[2];
     }
+  } else if constexpr (sizeof(T) == 2) {
+    store_windows<Lay::kLanes>(a, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s)]); });
+    store_windows<Lay::kLanes>(b, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s) + 1]); });
+    store_windows<Lay::kLanes>(c, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s) + 2]); });
   } else {
     for (int s = tid; s < steps; s += Lay::kLanes) {
       const compute_t<T>* p = src + Lay::point_slot(9 + 3 * s);

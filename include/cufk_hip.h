@@ -82,7 +82,10 @@ int cufk_reconstruct_fwd_flagged(int dtype, const void* lengths, const void* ang
 /*
  * Backward reconstruction: dL/d(lengths, angles, dihedrals) from grad_xyz (B, N, 3).
  * Replaces block.cu:331-365 (backward_cuda_impl) and block_backward_kernel
- * (block.cu:230-313).  The anchors receive no gradient (block.cu:427).
+ * (block.cu:230-313).  The anchors receive no gradient (block.cu:427).  Needs no saved output:
+ * each chain's positions are recomputed in the compute precision (float for float16/bfloat16)
+ * and the force/moment adjoint runs over them; chains failing the regularity test of
+ * cufk_reconstruct_fwd_flagged (applied to those positions) take the exact recompute.
  */
 int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
                          const void* p0, const void* first_direction, const void* initial_normal,
@@ -92,9 +95,10 @@ int cufk_reconstruct_bwd(int dtype, const void* lengths, const void* angles, con
 /*
  * Backward reconstruction given the forward's own output: chains with chain_regular[b] != 0
  * take the position-based adjoint over xyz (the force/moment form the reference's torsion
- * backward uses, torsion.cu:204-217), the others the exact recompute of cufk_reconstruct_bwd.
- * xyz and chain_regular must be exactly what cufk_reconstruct_fwd_flagged wrote for these
- * inputs.  Replaces block.cu:331-365 for callers that keep the forward output.
+ * backward uses, torsion.cu:204-217), the others the exact recompute.  For float16/bfloat16
+ * (never flagged) it behaves as cufk_reconstruct_bwd.  xyz and chain_regular must be exactly
+ * what cufk_reconstruct_fwd_flagged wrote for these inputs.  Replaces block.cu:331-365 for
+ * callers that keep the forward output.
  */
 int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angles, const void* dihedrals,
                                const void* p0, const void* first_direction, const void* initial_normal,
