@@ -207,6 +207,94 @@ Tensor apply_reconstruct(const Tensor& lengths, const Tensor& angles, const Tens
   return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
 }
 
+// ------------------------------------------------------------------ long chains
+
+// Segmented reconstruction without the 2048-step cap (no reference counterpart: its README:58
+// leaves long chains to a separate repository).  Same inputs, validation and gradients as
+// ReconstructAutograd; segment_steps 0 picks the library default.
+int64_t long_segment_steps(const Shape& shape, int64_t requested) {
+  const int64_t s = requested > 0 ? requested : cufk_long_segment_steps(shape.batch, shape.points);
+  TORCH_CHECK(s >= 1 && s <= 2048, "segment_steps must be in [1, 2048], got ", s);
+  return s;
+}
+
+Tensor long_buffer(int64_t doubles, const Tensor& ref) {
+  TORCH_CHECK(doubles >= 0, "shape exceeds int32 kernel limits");
+  return torch::empty({doubles}, ref.options().dtype(torch::kFloat64));
+}
+
+void long_forward(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Anchors& a,
+                  const Shape& shape, int64_t seg, const Tensor& xyz, const Tensor& state) {
+  check_status(cufk_reconstruct_long_fwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                         dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                         a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                         static_cast<double*>(state.data_ptr()), shape.batch, shape.points, seg,
+                                         current_stream(lengths)),
+               "cufk_reconstruct_long_fwd");
+}
+
+class LongReconstructAutograd : public torch::autograd::Function<LongReconstructAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
+                        Tensor p0, Tensor first_direction, Tensor initial_normal, int64_t segment_steps) {
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    const c10::DeviceGuard guard(lengths.device());
+    const int64_t seg = long_segment_steps(shape, segment_steps);
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    Tensor state = long_buffer(cufk_long_state_doubles(shape.batch, shape.points, seg), lengths);
+    long_forward(lengths, angles, dihedrals, a, shape, seg, xyz, state);
+    // As in ReconstructAutograd: the output is kept as a detached alias with its version; if
+    // the caller modified it in place, the backward recomputes it.
+    ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
+    ctx->saved_data["xyz"] = xyz.detach();
+    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["state"] = state;
+    ctx->saved_data["segment_steps"] = seg;
+    return xyz;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& lengths = saved[0];
+    const Tensor& angles = saved[1];
+    const Tensor& dihedrals = saved[2];
+    Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_points, lengths, "grad_points", true);
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true);
+    const c10::DeviceGuard guard(lengths.device());
+    const int64_t seg = ctx->saved_data["segment_steps"].toInt();
+    Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    Tensor state = ctx->saved_data["state"].toTensor();
+    if (xyz._version() != ctx->saved_data["xyz_version"].toInt()) {
+      xyz = torch::empty_like(xyz);
+      state = torch::empty_like(state);
+      long_forward(lengths, angles, dihedrals, a, shape, seg, xyz, state);
+    }
+    Tensor work = long_buffer(cufk_long_work_doubles(shape.batch, shape.points, seg), lengths);
+    Tensor grad_lengths = torch::empty_like(lengths);
+    Tensor grad_angles = torch::empty_like(angles);
+    Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    check_status(cufk_reconstruct_long_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                           dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                           a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                           static_cast<const double*>(state.data_ptr()), grad_points.data_ptr(),
+                                           static_cast<double*>(work.data_ptr()), grad_lengths.data_ptr(),
+                                           grad_angles.data_ptr(), grad_dihedrals.data_ptr(), shape.batch,
+                                           shape.points, seg, current_stream(lengths)),
+                 "cufk_reconstruct_long_bwd");
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
+  }
+};
+
+Tensor apply_reconstruct_long(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
+                              const Tensor& first_direction, const Tensor& initial_normal, int64_t segment_steps) {
+  return LongReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal,
+                                        segment_steps);
+}
+
 // ------------------------------------------------------------------ torsion
 
 cufk_torsion_consts consts_from(const std::vector<double>& packed) {
@@ -303,6 +391,10 @@ std::vector<int64_t> validate_torsion(const Tensor& raw_pairs, bool device) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("apply", &apply_reconstruct, "reconstruct autograd apply (block.cu:443-445)", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
+  m.def("apply_long", &apply_reconstruct_long, "segmented reconstruct for chains of any length", py::arg("lengths"),
+        py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"),
+        py::arg("segment_steps") = 0);
+  m.def("long_segment_steps", [](int64_t batch, int64_t points) { return cufk_long_segment_steps(batch, points); });
   py::class_<TorsionModule>(m, "TorsionModule")
       .def(py::init<const std::vector<double>&, const std::vector<double>&, const std::vector<double>&>(),
            py::arg("lengths"), py::arg("sin"), py::arg("cos"))

@@ -13,6 +13,7 @@
 #include <cstdint>
 
 #include "chain_ops.h"
+#include "long_chain_kernels.h"
 #include "reconstruct_kernels.h"
 #include "staging.h"
 #include "torsion_kernels.h"
@@ -108,6 +109,53 @@ int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0,
   });
 }
 
+// ---------------------------------------------------------------------------- long chains
+
+// Default segment length: the largest plan capacity (2048 steps) unless the grid would then
+// hold fewer than ~4 workgroups per CU; halved down to 256 steps until it does.
+constexpr int64_t kLongMinSegment = 256;
+constexpr int64_t kLongTargetGroups = 1024;
+// Grid extents of the long-chain launches count work-items in 32 bits.
+constexpr int64_t kLongMaxGroups = int64_t{UINT32_MAX} / 256;
+
+inline int64_t long_segments(int64_t points, int64_t seg_steps) { return (points - 3 + seg_steps - 1) / seg_steps; }
+
+template <typename T>
+int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, double* state,
+                   int64_t B, int N, int S, hipStream_t st) {
+  const int segs = static_cast<int>(long_segments(N, S));
+  const int rc = with_scan_plan(S, [&]<int W, int K>() {
+    hipLaunchKernelGGL((long_forward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
+                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, state, N, S, segs);
+    return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
+  });
+  if (rc != CUFK_OK) return rc;
+  hipLaunchKernelGGL(long_forward_frames_kernel<T>, dim3(static_cast<unsigned>((B + kLongThreads - 1) / kLongThreads)),
+                     dim3(kLongThreads), 0, st, L, A, p0, fd, n0, state, B, N, segs);
+  if (segs > 1)
+    hipLaunchKernelGGL(long_forward_place_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
+                       st, xyz, state, N, S, segs);
+  return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
+}
+
+template <typename T>
+int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                   const double* state, const T* g, double* work, T* gL, T* gA, T* gD, int64_t B, int N, int S,
+                   hipStream_t st) {
+  const int segs = static_cast<int>(long_segments(N, S));
+  if (segs > 1)
+    hipLaunchKernelGGL(long_backward_sums_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
+                       st, xyz, g, state, work, N, S, segs);
+  hipLaunchKernelGGL(long_backward_carry_kernel, dim3(static_cast<unsigned>((B + kLongThreads - 1) / kLongThreads)),
+                     dim3(kLongThreads), 0, st, state, work, B, segs);
+  if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
+  return with_scan_plan(S, [&]<int W, int K>() {
+    hipLaunchKernelGGL((long_backward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
+                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, g, gL, gA, gD, state, work, N, S, segs);
+    return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
+  });
+}
+
 // ---------------------------------------------------------------------------- torsion
 
 template <typename T>
@@ -138,6 +186,16 @@ inline int check_chain(int64_t batch, int64_t points) {
   if (batch < 0 || batch > INT32_MAX || points > INT32_MAX) return CUFK_ERR_SHAPE;
   if (points < 4) return CUFK_ERR_POINTS;
   if (points - 3 > kMaxSteps) return CUFK_ERR_STEPS;
+  return CUFK_OK;
+}
+
+// Long chains: no step cap, but in-row element offsets stay in int32 and the segment grid
+// within one launch.
+inline int check_long(int64_t batch, int64_t points, int64_t seg_steps) {
+  if (batch < 0 || batch > INT32_MAX || points > INT32_MAX / 3) return CUFK_ERR_SHAPE;
+  if (points < 4) return CUFK_ERR_POINTS;
+  if (seg_steps < 1 || seg_steps > kMaxSteps) return CUFK_ERR_SEGMENT;
+  if (batch * long_segments(points, seg_steps) > kLongMaxGroups) return CUFK_ERR_SHAPE;
   return CUFK_OK;
 }
 
@@ -283,6 +341,61 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
   });
 }
 
+int64_t cufk_long_segment_steps(int64_t batch, int64_t points) {
+  if (batch < 0 || points < 4) return 0;
+  int64_t S = kMaxSteps;
+  while (S > kLongMinSegment && batch * long_segments(points, S) < kLongTargetGroups) S /= 2;
+  return S;
+}
+
+int64_t cufk_long_state_doubles(int64_t batch, int64_t points, int64_t segment_steps) {
+  if (check_long(batch, points, segment_steps) != CUFK_OK) return -1;
+  return batch * long_segments(points, segment_steps) * kLongStateDoubles;
+}
+
+int64_t cufk_long_work_doubles(int64_t batch, int64_t points, int64_t segment_steps) {
+  if (check_long(batch, points, segment_steps) != CUFK_OK) return -1;
+  return batch * long_segments(points, segment_steps) * kLongWorkDoubles;
+}
+
+int cufk_reconstruct_long_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, void* xyz,
+                              double* state, int64_t batch, int64_t points, int64_t segment_steps, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_long(batch, points, segment_steps);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !xyz || !state)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return long_fwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                             cp<T>(initial_normal), mp<T>(xyz), state, batch, static_cast<int>(points),
+                             static_cast<int>(segment_steps), st);
+  });
+}
+
+int cufk_reconstruct_long_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, const void* xyz,
+                              const double* state, const void* grad_xyz, double* work, void* grad_lengths,
+                              void* grad_angles, void* grad_dihedrals, int64_t batch, int64_t points,
+                              int64_t segment_steps, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_long(batch, points, segment_steps);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !xyz || !state ||
+      !grad_xyz || !work || !grad_lengths || !grad_angles || !grad_dihedrals)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return long_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                             cp<T>(initial_normal), cp<T>(xyz), state, cp<T>(grad_xyz), work, mp<T>(grad_lengths),
+                             mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, static_cast<int>(points),
+                             static_cast<int>(segment_steps), st);
+  });
+}
+
 int cufk_max_steps(int dtype, int direction, int device) {
   (void)device;
   if (!valid_dtype(dtype)) return -CUFK_ERR_DTYPE;
@@ -301,6 +414,7 @@ const char* cufk_error_string(int status) {
     case CUFK_ERR_STRIDE: return "negative row stride";
     case CUFK_ERR_LAUNCH: return "kernel launch failed";
     case CUFK_ERR_DEVICE: return "device query failed";
+    case CUFK_ERR_SEGMENT: return "segment length must be in [1, 2048] local transforms";
     default: return "unknown status";
   }
 }

@@ -1,0 +1,233 @@
+// Long chains: more local transforms than one workgroup scans (the reference stops at 2048,
+// extension_utils.cuh:128-130; its README:58 leaves longer chains to a separate repository).
+//
+// The chain is cut into segments of S steps.  Each segment is scanned by one workgroup as a
+// chain of its own (forward_chain / exact_chain in their segmented form) and the segments are
+// joined by short per-chain passes in double.  No workgroup ever waits for another: every
+// dependency between segments crosses a kernel boundary.
+//
+// Segment j of chain b covers steps [jS, jS + n_j), n_j = min(S, steps - jS), i.e. places
+// points jS+3 .. jS+n_j+2; its "x2" is point jS+2, the last point before it.
+//
+// State, float64, per (chain, segment), written by the forward:
+//   [0..11]  the segment's own total transform (row-major rotation, then translation)
+//   [12..23] the world frame at the segment's x2: rotation (row-major), then x2 itself
+// Work, float64, per (chain, segment), used by the backward:
+//   [0..5]   F = sum g and M = sum (x - x2) x g over the segment's own points
+//   [6..11]  the same sums over every point after the segment, about the segment's x2
+//
+// Forward: segments (identity frame for j >= 1, local positions) -> frames -> place.
+// Backward: sums (saved positions) -> carry -> segments (exact adjoint with frame and carry).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "chain_ops.h"
+#include "reconstruct_kernels.h"
+#include "staging.h"
+
+namespace cufk_amd {
+
+constexpr int kLongStateDoubles = 24;
+constexpr int kLongWorkDoubles = 12;
+constexpr int kLongThreads = 256;  // per-point and per-chain passes
+
+struct SegmentOf {
+  int64_t chain;
+  int index;  // j
+  int first;  // first step, jS
+  int steps;  // n_j
+};
+
+// Workgroup g of a grid over (chain, segment j >= j0), chain-major.
+__device__ __forceinline__ SegmentOf segment_of(int64_t g, int points, int seg_steps, int segments, int j0) {
+  const int per = segments - j0;
+  SegmentOf s;
+  s.chain = g / per;
+  s.index = j0 + static_cast<int>(g - s.chain * per);
+  s.first = s.index * seg_steps;
+  const int left = points - 3 - s.first;
+  s.steps = left < seg_steps ? left : seg_steps;
+  return s;
+}
+
+// ---------------------------------------------------------------------------- forward
+
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void long_forward_segments_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    T* __restrict__ xyz, double* __restrict__ state, int points, int seg_steps, int segments) {
+  const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 0);
+  const int64_t b = s.chain;
+  forward_chain<T, Layout<W, K, Pad>, true>(
+      lengths + b * (points - 1) + s.first, angles + b * (points - 2) + s.first, dihedrals + b * (points - 3) + s.first,
+      p0, first_direction, initial_normal, xyz + (b * points + s.first) * 3, nullptr, s.steps + 3, s.index == 0,
+      state + (b * segments + s.index) * kLongStateDoubles);
+}
+
+// One thread per chain: the world frame at every segment's x2, composed in double from the
+// first frame (the one the head segment used) and the segment totals.
+template <typename T>
+__global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ p0,
+    const T* __restrict__ first_direction, const T* __restrict__ initial_normal, double* __restrict__ state,
+    int64_t batch, int points, int segments) {
+  using R = compute_t<T>;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * kLongThreads + threadIdx.x;
+  if (b >= batch) return;
+  const T* Lr = lengths + b * (points - 1);
+  const T* Ar = angles + b * (points - 2);
+  const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+  double m[9], o[3] = {static_cast<double>(ff.p2.x), static_cast<double>(ff.p2.y), static_cast<double>(ff.p2.z)};
+  for (int i = 0; i < 9; ++i) m[i] = static_cast<double>(ff.frame[i]);
+  double* st = state + b * segments * kLongStateDoubles;
+  for (int j = 0; j < segments; ++j, st += kLongStateDoubles) {
+    for (int i = 0; i < 9; ++i) st[12 + i] = m[i];
+    for (int i = 0; i < 3; ++i) st[21 + i] = o[i];
+    if (j + 1 == segments) break;
+    // (m, o) o total
+    double nm[9];
+    for (int r = 0; r < 3; ++r) {
+      o[r] += m[3 * r] * st[9] + m[3 * r + 1] * st[10] + m[3 * r + 2] * st[11];
+      for (int c = 0; c < 3; ++c) nm[3 * r + c] = m[3 * r] * st[c] + m[3 * r + 1] * st[3 + c] + m[3 * r + 2] * st[6 + c];
+    }
+    for (int i = 0; i < 9; ++i) m[i] = nm[i];
+  }
+}
+
+// Segments j >= 1: local positions y -> x2 + F y in world coordinates, in place.
+template <typename T>
+__global__ __launch_bounds__(kLongThreads) void long_forward_place_kernel(T* __restrict__ xyz,
+                                                                         const double* __restrict__ state, int points,
+                                                                         int seg_steps, int segments) {
+  const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 1);
+  const double* f = state + (s.chain * segments + s.index) * kLongStateDoubles + 12;
+  double m[9], o[3];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) m[i] = f[i];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) o[i] = f[9 + i];
+  T* x = xyz + (s.chain * points + s.first + 3) * 3;
+  for (int i = threadIdx.x; i < s.steps; i += kLongThreads) {
+    const double y0 = static_cast<double>(widen(x[3 * i]));
+    const double y1 = static_cast<double>(widen(x[3 * i + 1]));
+    const double y2 = static_cast<double>(widen(x[3 * i + 2]));
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      x[3 * i + r] = narrow<T>(static_cast<compute_t<T>>(o[r] + m[3 * r] * y0 + m[3 * r + 1] * y1 + m[3 * r + 2] * y2));
+  }
+}
+
+// ---------------------------------------------------------------------------- backward
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// Segments j >= 1: F and M about the segment's x2 over its own points, from the saved
+// positions, in double.
+template <typename T>
+__global__ __launch_bounds__(kLongThreads) void long_backward_sums_kernel(const T* __restrict__ xyz,
+                                                                         const T* __restrict__ grad_xyz,
+                                                                         const double* __restrict__ state,
+                                                                         double* __restrict__ work, int points,
+                                                                         int seg_steps, int segments) {
+  __shared__ double part[kLongThreads / 64][6];
+  const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 1);
+  const int64_t at = s.chain * segments + s.index;
+  const double* o = state + at * kLongStateDoubles + 21;
+  const double o0 = o[0], o1 = o[1], o2 = o[2];
+  const int64_t base = (s.chain * points + s.first + 3) * 3;
+  const T* x = xyz + base;
+  const T* g = grad_xyz + base;
+  double acc[6] = {0, 0, 0, 0, 0, 0};
+  for (int i = threadIdx.x; i < s.steps; i += kLongThreads) {
+    const double d0 = static_cast<double>(widen(x[3 * i])) - o0;
+    const double d1 = static_cast<double>(widen(x[3 * i + 1])) - o1;
+    const double d2 = static_cast<double>(widen(x[3 * i + 2])) - o2;
+    const double g0 = static_cast<double>(widen(g[3 * i]));
+    const double g1 = static_cast<double>(widen(g[3 * i + 1]));
+    const double g2 = static_cast<double>(widen(g[3 * i + 2]));
+    acc[0] += g0;
+    acc[1] += g1;
+    acc[2] += g2;
+    acc[3] += d1 * g2 - d2 * g1;
+    acc[4] += d2 * g0 - d0 * g2;
+    acc[5] += d0 * g1 - d1 * g0;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const double v = wave_sum_f64(acc[k]);
+    if (lane == 0) part[wave][k] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    double v = 0;
+#pragma unroll
+    for (int w = 0; w < kLongThreads / 64; ++w) v += part[w][threadIdx.x];
+    work[at * kLongWorkDoubles + threadIdx.x] = v;
+  }
+}
+
+// One thread per chain: the suffix carry of every segment, last to first, each moved to its
+// segment's x2 (M about a = M about b + (b - a) x F).
+__global__ __launch_bounds__(kLongThreads) void long_backward_carry_kernel(const double* __restrict__ state,
+                                                                          double* __restrict__ work, int64_t batch,
+                                                                          int segments) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * kLongThreads + threadIdx.x;
+  if (b >= batch) return;
+  double F[3] = {0, 0, 0}, M[3] = {0, 0, 0};
+  for (int j = segments - 1; j >= 0; --j) {
+    const int64_t at = b * segments + j;
+    double* w = work + at * kLongWorkDoubles;
+    for (int i = 0; i < 3; ++i) {
+      w[6 + i] = F[i];
+      w[9 + i] = M[i];
+    }
+    if (j == 0) break;
+    // Add segment j's own sums, then move from x2 of segment j to x2 of segment j-1.
+    for (int i = 0; i < 3; ++i) {
+      F[i] += w[i];
+      M[i] += w[3 + i];
+    }
+    const double* oj = state + at * kLongStateDoubles + 21;
+    const double* op = state + (at - 1) * kLongStateDoubles + 21;
+    const double d[3] = {oj[0] - op[0], oj[1] - op[1], oj[2] - op[2]};
+    M[0] += d[1] * F[2] - d[2] * F[1];
+    M[1] += d[2] * F[0] - d[0] * F[2];
+    M[2] += d[0] * F[1] - d[1] * F[0];
+  }
+}
+
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
+    T* __restrict__ grad_dihedrals, const double* __restrict__ state, const double* __restrict__ work, int points,
+    int seg_steps, int segments) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K, Pad>;
+  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];
+  __shared__ __align__(16) R gstage[Lay::kPointRow];
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
+  __shared__ int wide_vote[W];
+  const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 0);
+  const int64_t b = s.chain;
+  const int64_t at = b * segments + s.index;
+  exact_chain<T, Lay, true>(lengths + b * (points - 1) + s.first, angles + b * (points - 2) + s.first,
+                            dihedrals + b * (points - 3) + s.first, p0, first_direction, initial_normal,
+                            grad_xyz + (b * points + s.first) * 3, grad_lengths + b * (points - 1) + s.first,
+                            grad_angles + b * (points - 2) + s.first, grad_dihedrals + b * (points - 3) + s.first,
+                            pstage, gstage, wave_total, wave_sum, wide_vote, s.steps + 3, s.index == 0,
+                            state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6);
+}
+
+}  // namespace cufk_amd

@@ -47,18 +47,43 @@ template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
   return fmax(m, fabs(x.z));
 }
 
+// total = excl o q in double (row-major rotation, then translation).
+template <typename R>
+__device__ __forceinline__ void store_total(double* __restrict__ total, const Rigid<R>& excl, const Rigid<double>& q) {
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      total[3 * r + c] = static_cast<double>(excl.m[3 * r]) * q.m[c] + static_cast<double>(excl.m[3 * r + 1]) * q.m[3 + c] +
+                         static_cast<double>(excl.m[3 * r + 2]) * q.m[6 + c];
+    total[9 + r] = static_cast<double>(excl.v[r]) + static_cast<double>(excl.m[3 * r]) * q.v[0] +
+                   static_cast<double>(excl.m[3 * r + 1]) * q.v[1] + static_cast<double>(excl.m[3 * r + 2]) * q.v[2];
+  }
+}
+
 // ============================================================================ forward
 
-// x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v.  When
-// `regular` is non-null, regular[row] receives the fast-path predicate for the chain.
-// Rows are staged through LDS (coalesced 16-byte streams in and out).
-template <typename T, int W, int K, int Pad = 4>
-__global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
-    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
-    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
-    T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
+// x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v, for one
+// chain (Lr, Ar, Dr: its parameter rows, out: its (points, 3) row).  When `regular` is
+// non-null, *regular receives the fast-path predicate for the chain.  Rows are staged through
+// LDS (coalesced 16-byte streams in and out).
+//
+// Segmented: the rows are a segment of a longer chain, seen as a chain of its own whose
+// points 0..2 are the three points before the segment.  The first segment (head) runs as a
+// whole chain; the others start from the identity frame at the origin, so they write their
+// points in the frame of the segment start (x2 of the view) and leave points 0..2 alone.
+// Every segment writes its total transform (row-major rotation, then translation; double) to
+// total[0..11].
+template <typename T, typename Lay, bool Segmented>
+__device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
+                                              const T* __restrict__ Dr, const T* __restrict__ p0,
+                                              const T* __restrict__ first_direction,
+                                              const T* __restrict__ initial_normal, T* __restrict__ out,
+                                              uint8_t* __restrict__ regular, int points, bool head,
+                                              double* __restrict__ total) {
   using R = compute_t<T>;
-  using Lay = Layout<W, K, Pad>;
+  constexpr int W = Lay::kWaves;
+  constexpr int K = Lay::kItems;
   constexpr int kStage = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
   __shared__ __align__(16) R stage[kStage];
   __shared__ R wave_total[W][12];
@@ -68,11 +93,6 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   __shared__ SinCosEntry sc_table[kSinCosTable];
 
   const int steps = points - 3;
-  const int64_t row = blockIdx.x;
-  const T* Lr = lengths + row * (points - 1);
-  const T* Ar = angles + row * (points - 2);
-  const T* Dr = dihedrals + row * (points - 3);
-  T* out = xyz + row * points * 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -88,13 +108,18 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid);
   FirstFrame<R> ff;
   if (wave == 0) {
-    ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-    if (lane == 0) {
+    if (!Segmented || head) {
+      ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+      if (lane == 0) {
 #pragma unroll
-      for (int i = 0; i < 9; ++i) base[i] = ff.frame[i];
-      base[9] = ff.p2.x;
-      base[10] = ff.p2.y;
-      base[11] = ff.p2.z;
+        for (int i = 0; i < 9; ++i) base[i] = ff.frame[i];
+        base[9] = ff.p2.x;
+        base[10] = ff.p2.y;
+        base[11] = ff.p2.z;
+      }
+    } else if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 12; ++i) base[i] = (i == 0 || i == 4 || i == 8) ? R(1) : R(0);
     }
   }
   wide = block_any<W>(wide, wide_vote, lane, wave);
@@ -138,6 +163,9 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
   // lane_carry's barrier also publishes base[] and retires every read of the staged step
   // rows, which the point row below overwrites.
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
+  if constexpr (Segmented) {
+    if (count > 0 && count + s0 == steps) store_total(total, excl, q);  // the lane with the last step
+  }
   R F[9];
 #pragma unroll
   for (int i = 0; i < 9; ++i) F[i] = base[i];
@@ -165,7 +193,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
         xmax = abs_max3(xmax, x);
       }
     }
-    if (tid == 0) {
+    if (tid == 0 && (!Segmented || head)) {
       stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
       stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
       stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
@@ -198,9 +226,21 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
       }
       reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * m;
     }
-    regular[row] = reg ? 1 : 0;
+    *regular = reg ? 1 : 0;
   }
-  store_point_row<Lay>(out, stage, points, tid);
+  store_point_row<Lay>(out, stage, points, tid, !Segmented || head);
+}
+
+template <typename T, int W, int K, int Pad = 4>
+__global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
+  const int64_t row = blockIdx.x;
+  forward_chain<T, Layout<W, K, Pad>, false>(lengths + row * (points - 1), angles + row * (points - 2),
+                                             dihedrals + row * (points - 3), p0, first_direction, initial_normal,
+                                             xyz + row * points * 3, regular != nullptr ? regular + row : nullptr,
+                                             points, true, nullptr);
 }
 
 // ============================================================================ exact backward
@@ -214,7 +254,12 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
 // the workgroup calls this; pstage holds 3 step rows, gstage one point row.  The reverse walk
 // recomputes each step's sin/cos instead of keeping them in registers, so this path does not
 // raise the register count of a kernel that also carries the position-based path.
-template <typename T, typename Lay>
+//
+// Segmented: the rows are a segment of a longer chain (as in forward_chain).  A segment other
+// than the first (head) starts from the world rotation frame[0..8] (row-major) at its x2,
+// and carry[0..5] holds F and M (about that x2) of every point after the segment; only the
+// head writes the first-frame terms.
+template <typename T, typename Lay, bool Segmented = false>
 __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                             const T* __restrict__ Dr, const T* __restrict__ p0,
                                             const T* __restrict__ first_direction,
@@ -223,7 +268,8 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
                                             compute_t<T>* pstage, compute_t<T>* gstage,
                                             compute_t<T> (&wave_total)[Lay::kWaves][12],
                                             compute_t<T> (&wave_sum)[Lay::kWaves][6], int (&wide_vote)[Lay::kWaves],
-                                            int points) {
+                                            int points, bool head = true, const double* __restrict__ frame = nullptr,
+                                            const double* __restrict__ carry = nullptr) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -243,7 +289,16 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
     const T* const gsrc[1] = {Gr};
     load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
   }
-  const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+  FirstFrame<R> ff;
+  R Fm[9];  // world rotation at x2
+  if (!Segmented || head) {
+    ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) Fm[i] = ff.frame[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) Fm[i] = static_cast<R>(frame[i]);
+  }
   wide = block_any<W>(wide, wide_vote, lane, wave);
 
   // Pass 1: lane-local scan (double); Y = sum_i y_i g_i^T and sum_i g_i.
@@ -287,9 +342,9 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
   for (int r = 0; r < 3; ++r) {
 #pragma unroll
     for (int c = 0; c < 3; ++c)
-      R0[3 * r + c] = ff.frame[3 * r] * excl.m[c] + ff.frame[3 * r + 1] * excl.m[3 + c] + ff.frame[3 * r + 2] * excl.m[6 + c];
+      R0[3 * r + c] = Fm[3 * r] * excl.m[c] + Fm[3 * r + 1] * excl.m[3 + c] + Fm[3 * r + 2] * excl.m[6 + c];
   }
-  const V3<R> X0 = rot_apply(ff.frame, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+  const V3<R> X0 = rot_apply(Fm, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
 
   // Lane moment sum_i (X0 + R0 y_i) x g_i = X0 x gsum + axial part of R0 Y.
   R Z[9];
@@ -315,6 +370,10 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 
   // Pass 2: walk the lane's steps backwards; the outputs of step s replace g_{s+3} in LDS.
   V3<R> Fs = tail.f, Ms = tail.m;
+  if constexpr (Segmented) {
+    Fs = Fs + V3<R>{static_cast<R>(carry[0]), static_cast<R>(carry[1]), static_cast<R>(carry[2])};
+    Ms = Ms + V3<R>{static_cast<R>(carry[3]), static_cast<R>(carry[4]), static_cast<R>(carry[5])};
+  }
   auto pass2 = [&]<bool Checked>() {
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
@@ -345,7 +404,7 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
     pass2.template operator()<true>();
   else
     pass2.template operator()<false>();
-  if (tid == 0) {
+  if (tid == 0 && (!Segmented || head)) {
     // First-frame parameters (block.cu:206-228); x2 is the origin, so M_2 = M_3.
     const V3<R> g1 = load3(&gstage[3]);
     const V3<R> g2 = load3(&gstage[6]);

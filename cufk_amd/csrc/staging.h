@@ -326,12 +326,12 @@ __device__ __forceinline__ void store_step_row(T* __restrict__ dst, const comput
   }
 }
 
-// dst[e] = src[point_slot(e)] for e in [0, 3*points).
+// dst[e] = src[point_slot(e)] for e in [0, 3*points); without `head`, points 0..2 are left alone.
 template <typename Lay, typename T>
 __device__ __forceinline__ void store_point_row(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int points,
-                                                int tid) {
+                                                int tid, bool head = true) {
   const int n = 3 * points - 9;
-  if (tid < 9) dst[tid] = narrow<T>(src[tid]);
+  if (head && tid < 9) dst[tid] = narrow<T>(src[tid]);
   if constexpr (std::is_same_v<T, float>) {
     const int groups = n >> 2;
     for (int g = tid; g < groups; g += Lay::kLanes)

@@ -73,3 +73,41 @@ def reconstruct(
         initial_normal,
     )
     return xyz[0] if single else xyz
+
+
+def reconstruct_long(
+    lengths: torch.Tensor,
+    angles: torch.Tensor,
+    dihedrals: torch.Tensor,
+    p0: torch.Tensor | None = None,
+    first_direction: torch.Tensor | None = None,
+    initial_normal: torch.Tensor | None = None,
+    segment_steps: int | None = None,
+) -> torch.Tensor:
+    r"""``reconstruct`` for chains of any length (N >= 4, no 2051-point cap).
+
+    Same arguments, defaults, validation and gradients as :func:`reconstruct`.  The chain is
+    cut into segments of ``segment_steps`` local transforms (1..2048; by default 2048, halved
+    down to 256 while fewer than 1024 segments would run), each reconstructed by one
+    workgroup and joined in float64; the backward applies the exact adjoint per segment.
+    Without ``segment_steps``, chains of at most 2051 points take :func:`reconstruct` itself.
+
+    The reference has no counterpart (its README leaves long chains to a separate
+    repository); this extends its interface rather than mirroring it.
+    """
+    if segment_steps is None and lengths.shape[-1] + 1 <= BLOCK_SCAN_MAX_POINT_COUNT:
+        return reconstruct(lengths, angles, dihedrals, p0, first_direction, initial_normal)
+    lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
+    p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
+    first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
+    initial_normal = _anchor(initial_normal, (0.0, 0.0, 1.0), lengths)
+    xyz = _C.apply_long(
+        lengths.contiguous(),
+        angles.contiguous(),
+        dihedrals.contiguous(),
+        p0,
+        first_direction,
+        initial_normal,
+        0 if segment_steps is None else int(segment_steps),
+    )
+    return xyz[0] if single else xyz

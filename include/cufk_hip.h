@@ -40,7 +40,8 @@ enum cufk_status {
   CUFK_ERR_NULL = 5,        /* a required pointer is NULL while B > 0 */
   CUFK_ERR_STRIDE = 6,      /* raw-pair row stride shorter than the row */
   CUFK_ERR_LAUNCH = 7,      /* kernel launch failed (C10_CUDA_KERNEL_LAUNCH_CHECK, block.cu:327) */
-  CUFK_ERR_DEVICE = 8       /* device query failed */
+  CUFK_ERR_DEVICE = 8,      /* device query failed */
+  CUFK_ERR_SEGMENT = 9      /* long-chain segment length outside [1, 2048] */
 };
 
 /* Direction argument of cufk_max_steps. */
@@ -120,6 +121,34 @@ int cufk_torsion_fwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
 int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const void* xyz, const void* grad_xyz,
                      void* grad_raw, int64_t grad_raw_stride, const cufk_torsion_consts* consts, int64_t batch,
                      int64_t points, void* stream);
+
+/*
+ * Long chains (any N >= 4; no step cap).  The reference stops at 2048 local transforms
+ * (extension_utils.cuh:128-130) and its README:58 points long chains to a separate repository
+ * (coord_scan_repro, not part of it), so these have no reference counterpart; they extend
+ * cufk_reconstruct_fwd / _bwd with the same inputs, outputs and conventions.
+ *
+ * The chain is cut into segments of segment_steps local transforms (1..2048), each scanned by
+ * one workgroup, joined by short per-chain passes in double.  The caller provides two float64
+ * buffers: `state` (cufk_long_state_doubles elements), written by the forward and read by the
+ * backward of the same inputs and segment_steps; and `work` (cufk_long_work_doubles
+ * elements), scratch for the backward.  Neither needs initialising.  The backward takes the
+ * forward's xyz and applies the exact adjoint in every segment.
+ */
+/* Default segment length for (batch, points): 2048, halved (down to 256) while the grid would
+ * hold fewer than 1024 segments.  0 for invalid shapes. */
+int64_t cufk_long_segment_steps(int64_t batch, int64_t points);
+/* Sizes of the state and work buffers in doubles, or -1 for invalid arguments. */
+int64_t cufk_long_state_doubles(int64_t batch, int64_t points, int64_t segment_steps);
+int64_t cufk_long_work_doubles(int64_t batch, int64_t points, int64_t segment_steps);
+int cufk_reconstruct_long_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, void* xyz,
+                              double* state, int64_t batch, int64_t points, int64_t segment_steps, void* stream);
+int cufk_reconstruct_long_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, const void* xyz,
+                              const double* state, const void* grad_xyz, double* work, void* grad_lengths,
+                              void* grad_angles, void* grad_dihedrals, int64_t batch, int64_t points,
+                              int64_t segment_steps, void* stream);
 
 /*
  * Largest step count (N-3) accepted for (dtype, direction) on `device`, or a negative

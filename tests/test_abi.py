@@ -27,6 +27,13 @@ def lib():
     lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
+    lib.cufk_reconstruct_long_fwd.argtypes = [ctypes.c_int] + [vp] * 8 + [i64, i64, i64, vp]
+    lib.cufk_reconstruct_long_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, i64, vp]
+    for name in ("cufk_long_state_doubles", "cufk_long_work_doubles"):
+        getattr(lib, name).argtypes = [i64, i64, i64]
+        getattr(lib, name).restype = i64
+    lib.cufk_long_segment_steps.argtypes = [i64, i64]
+    lib.cufk_long_segment_steps.restype = i64
     lib.cufk_error_string.restype = ctypes.c_char_p
     lib.cufk_version.restype = ctypes.c_char_p
     return lib
@@ -34,17 +41,22 @@ def lib():
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cufk_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(cufk_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == [
         "cufk_error_string",
+        "cufk_long_segment_steps",
+        "cufk_long_state_doubles",
+        "cufk_long_work_doubles",
         "cufk_max_steps",
         "cufk_reconstruct_bwd",
         "cufk_reconstruct_bwd_saved",
         "cufk_reconstruct_fwd",
         "cufk_reconstruct_fwd_flagged",
+        "cufk_reconstruct_long_bwd",
+        "cufk_reconstruct_long_fwd",
         "cufk_torsion_bwd",
         "cufk_torsion_fwd",
         "cufk_version",
@@ -108,3 +120,41 @@ def test_torsion_status_paths(lib):
     b = lib.cufk_torsion_bwd
     assert b(0, p, 14, p, p, p, -3, p, 2, 10, null) == ERR_STRIDE
     assert b(3, p, 14, p, p, p, 14, p, 2, 3, null) == ERR_POINTS
+
+
+ERR_SEGMENT = 9
+
+
+def test_long_sizes_and_default_segments(lib):
+    seg = lib.cufk_long_segment_steps
+    assert seg(4096, 2049) == 2048  # 4096 chains x 1 segment already fill the grid
+    assert seg(1, 100000) == 256  # 1 chain: halved down to the 256-step floor (391 segments)
+    assert seg(64, 131072) == 2048  # 64 x 64 segments
+    assert seg(16, 65536) == 1024  # 16 x 32 = 512 < 1024 at 2048; 16 x 64 at 1024
+    assert seg(0, 10) == 256 and seg(4, 3) == 0 and seg(-1, 10) == 0
+    # state: 24 doubles, work: 12 doubles per (chain, segment); segments = ceil((N-3)/S)
+    assert lib.cufk_long_state_doubles(3, 5003, 1000) == 3 * 5 * 24
+    assert lib.cufk_long_work_doubles(3, 5003, 1000) == 3 * 5 * 12
+    assert lib.cufk_long_state_doubles(3, 5004, 1000) == 3 * 6 * 24
+    assert lib.cufk_long_state_doubles(3, 5004, 0) == -1
+    assert lib.cufk_long_state_doubles(3, 5004, 2049) == -1
+    assert lib.cufk_long_state_doubles(3, 3, 16) == -1
+    assert lib.cufk_long_state_doubles(2, 2**31 // 3 + 1, 2048) == -1  # in-row offsets past int32
+
+
+def test_long_status_paths(lib):
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_long_fwd
+    assert f(9, p, p, p, p, p, p, p, p, 4, 10, 4, null) == ERR_DTYPE
+    assert f(0, p, p, p, p, p, p, p, p, 4, 3, 4, null) == ERR_POINTS
+    assert f(0, p, p, p, p, p, p, p, p, 4, 10, 0, null) == ERR_SEGMENT
+    assert f(0, p, p, p, p, p, p, p, p, 4, 10, 2049, null) == ERR_SEGMENT
+    assert f(0, p, p, p, p, p, p, p, null, 4, 10, 4, null) == ERR_NULL  # state is required
+    assert f(0, p, p, p, p, p, p, p, p, 0, 10, 4, null) == OK
+    assert f(0, p, p, p, p, p, p, p, p, 2**20, 2**20, 1, null) == ERR_SHAPE  # grid past 32 bits
+    b = lib.cufk_reconstruct_long_bwd
+    assert b(0, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 10, 4, null) == ERR_NULL  # work is required
+    assert b(0, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 10, 0, null) == ERR_SEGMENT
+    assert b(0, p, p, p, p, p, p, p, p, p, p, p, p, p, 0, 10, 4, null) == OK
+    assert lib.cufk_error_string(ERR_SEGMENT) == b"segment length must be in [1, 2048] local transforms"

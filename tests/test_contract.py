@@ -36,6 +36,7 @@ def validate(L, A, D, p0=None, fd=None, n0=None):
 def test_public_surface():
     assert cufk_amd.__all__ == ["BLOCK_SCAN_MAX_POINT_COUNT", "__version__", "compile_torsion", "reconstruct"]
     assert cufk_amd.BLOCK_SCAN_MAX_POINT_COUNT == 2051
+    assert callable(cufk_amd.reconstruct_long)  # extension, outside the reference's __all__
     assert cufk_amd.__version__ == "0.1.0"
     assert _C.library_version() == "0.1.0"
 
