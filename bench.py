@@ -21,9 +21,10 @@ HBM bytes per launch the rocprofv3 FETCH_SIZE and WRITE_SIZE counters read for t
 copied from the committed summaries under profiles/ (MEASURED_TRAFFIC below).
 
 The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host on a bounded
-sample of chains of the same shape (128-chain chunks until about 15 s of work), scaled to atoms/s.
+sample of chains of the same shape (chunks of about 128 x 2049 points until about 15 s of work),
+scaled to atoms/s.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long]
 """
 
 from __future__ import annotations
@@ -46,6 +47,9 @@ CONFIGS = {
     "c3": ("torsion", "float32", 8192, 771),
     "c4_bf16": ("reconstruct", "bfloat16", 16384, 1026),
     "c4_fp16": ("reconstruct", "float16", 16384, 1026),
+    # Past the 2051-point cap (reconstruct_long): C2's atom count as 64 chains of 131075 points,
+    # 64 segments of 2048 steps each.
+    "long": ("long", "float32", 64, 131075),
 }
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
@@ -124,7 +128,7 @@ def cpu_baseline(kind, B, N, sample, seconds):
 
     Chains are processed in chunks of at most 128 (bounding memory).  With sample == 0,
     chunks run until about `seconds` of work is done or B chains are covered; otherwise exactly
-    `sample` chains.  A 4-chain warm-up is not counted.
+    `sample` chains.  A 4-chain warm-up (1 chain for chains past 65k points) is not counted.
     Returns (atoms/s, chains, wall seconds, cpu seconds)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import nerf64 as o
@@ -146,12 +150,13 @@ def cpu_baseline(kind, B, N, sample, seconds):
             o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **an)
         return time.perf_counter() - t0, time.process_time() - c0
 
-    chunk(4, 1000)
+    per_chunk = max(1, min(128, 128 * 2049 // N))  # about 128 x 2049 points per chunk
+    chunk(4 if per_chunk >= 4 else 1, 1000)
     limit = sample if sample > 0 else B
     wall = cpu = 0.0
     done = 0
     while done < limit and (sample > 0 or wall < seconds):
-        n = min(128, limit - done)
+        n = min(per_chunk, limit - done)
         w, c = chunk(n, 2 + done)
         wall += w
         cpu += c
@@ -189,7 +194,50 @@ def main():
 
     # One entry per input set: the autograd step and the two C-ABI calls it makes.
     steps, fwds, bwds, regular = [], [], [], []
-    if kind == "reconstruct":
+    if kind == "long":
+        # Algorithmic bytes as for reconstruct; the segment joins (placement, segment sums)
+        # are extra traffic the roofline fraction is charged with.
+        fwd_bytes = s * B * (6 * N - 6)
+        bwd_bytes = s * B * (9 * N - 12)
+        lib.cufk_long_segment_steps.restype = i64
+        seg = lib.cufk_long_segment_steps(i64(B), i64(N))
+        lib.cufk_long_state_doubles.restype = i64
+        lib.cufk_long_work_doubles.restype = i64
+        n_state = lib.cufk_long_state_doubles(i64(B), i64(N), i64(seg))
+        n_work = lib.cufk_long_work_doubles(i64(B), i64(N), i64(seg))
+        assert n_state > 0 and n_work > 0
+        for k in range(nsets):
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype)
+            for t in (L, A, D):
+                t.requires_grad_(True)
+
+            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
+                xyz = cufk_amd.reconstruct_long(L, A, D, p0, fd, n0)
+                if mark is not None:
+                    mark.record()
+                return torch.autograd.grad(xyz, (L, A, D), g)
+
+            xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+            state = torch.empty(n_state, device=device, dtype=torch.float64)
+            work = torch.empty(n_work, device=device, dtype=torch.float64)
+            gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+
+            def fwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, state=state):
+                rc = lib.cufk_reconstruct_long_fwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(state),
+                                                   i64(B), i64(N), i64(seg), st)
+                assert rc == 0, rc
+
+            def bwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, state=state, g=g, work=work, gL=gL, gA=gA,
+                    gD=gD):
+                rc = lib.cufk_reconstruct_long_bwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(state),
+                                                   P(g), P(work), P(gL), P(gA), P(gD), i64(B), i64(N), i64(seg), st)
+                assert rc == 0, rc
+
+            fwd(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))  # state for the ABI backward
+            steps.append(step)
+            fwds.append(fwd)
+            bwds.append(bwd)
+    elif kind == "reconstruct":
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
         for k in range(nsets):

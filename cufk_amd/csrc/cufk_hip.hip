@@ -130,7 +130,8 @@ int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
   });
   if (rc != CUFK_OK) return rc;
-  hipLaunchKernelGGL(long_forward_frames_kernel<T>, dim3(static_cast<unsigned>((B + kLongThreads - 1) / kLongThreads)),
+  constexpr int64_t kChainsPerGroup = kLongThreads / 64;  // one wave per chain
+  hipLaunchKernelGGL(long_forward_frames_kernel<T>, dim3(static_cast<unsigned>((B + kChainsPerGroup - 1) / kChainsPerGroup)),
                      dim3(kLongThreads), 0, st, L, A, p0, fd, n0, state, B, N, segs);
   if (segs > 1)
     hipLaunchKernelGGL(long_forward_place_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
@@ -146,7 +147,8 @@ int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
   if (segs > 1)
     hipLaunchKernelGGL(long_backward_sums_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
                        st, xyz, g, state, work, N, S, segs);
-  hipLaunchKernelGGL(long_backward_carry_kernel, dim3(static_cast<unsigned>((B + kLongThreads - 1) / kLongThreads)),
+  constexpr int64_t kChainsPerGroup = kLongThreads / 64;  // one wave per chain
+  hipLaunchKernelGGL(long_backward_carry_kernel, dim3(static_cast<unsigned>((B + kChainsPerGroup - 1) / kChainsPerGroup)),
                      dim3(kLongThreads), 0, st, state, work, B, segs);
   if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
   return with_scan_plan(S, [&]<int W, int K>() {

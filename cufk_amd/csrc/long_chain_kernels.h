@@ -68,33 +68,54 @@ __global__ __launch_bounds__(64 * W) void long_forward_segments_kernel(
       state + (b * segments + s.index) * kLongStateDoubles);
 }
 
-// One thread per chain: the world frame at every segment's x2, composed in double from the
-// first frame (the one the head segment used) and the segment totals.
+// One wave per chain: the world frame at every segment's x2, composed in double from the
+// first frame (the one the head segment used) and the segment totals.  Lane l handles
+// segment 64c + l of chunk c: an ordered wave scan of the totals, then the running frame of
+// the earlier chunks in front.
 template <typename T>
 __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ p0,
     const T* __restrict__ first_direction, const T* __restrict__ initial_normal, double* __restrict__ state,
     int64_t batch, int points, int segments) {
   using R = compute_t<T>;
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * kLongThreads + threadIdx.x;
-  if (b >= batch) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * (kLongThreads / 64) + (threadIdx.x >> 6);
+  if (b >= batch) return;  // uniform per wave
   const T* Lr = lengths + b * (points - 1);
   const T* Ar = angles + b * (points - 2);
   const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-  double m[9], o[3] = {static_cast<double>(ff.p2.x), static_cast<double>(ff.p2.y), static_cast<double>(ff.p2.z)};
-  for (int i = 0; i < 9; ++i) m[i] = static_cast<double>(ff.frame[i]);
+  Rigid<double> run;  // world frame at x2 of the chunk's first segment
+#pragma unroll
+  for (int i = 0; i < 9; ++i) run.m[i] = static_cast<double>(ff.frame[i]);
+  run.v[0] = static_cast<double>(ff.p2.x);
+  run.v[1] = static_cast<double>(ff.p2.y);
+  run.v[2] = static_cast<double>(ff.p2.z);
   double* st = state + b * segments * kLongStateDoubles;
-  for (int j = 0; j < segments; ++j, st += kLongStateDoubles) {
-    for (int i = 0; i < 9; ++i) st[12 + i] = m[i];
-    for (int i = 0; i < 3; ++i) st[21 + i] = o[i];
-    if (j + 1 == segments) break;
-    // (m, o) o total
-    double nm[9];
-    for (int r = 0; r < 3; ++r) {
-      o[r] += m[3 * r] * st[9] + m[3 * r + 1] * st[10] + m[3 * r + 2] * st[11];
-      for (int c = 0; c < 3; ++c) nm[3 * r + c] = m[3 * r] * st[c] + m[3 * r + 1] * st[3 + c] + m[3 * r + 2] * st[6 + c];
+  for (int j0 = 0; j0 < segments; j0 += 64) {
+    const int j = j0 + lane;
+    Rigid<double> t = rigid_identity<double>();
+    if (j < segments) {
+      const double* tj = st + j * kLongStateDoubles;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) t.m[i] = tj[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) t.v[i] = tj[9 + i];
     }
-    for (int i = 0; i < 9; ++i) m[i] = nm[i];
+    const Rigid<double> incl = wave_prefix(t);
+    const Rigid<double> f = compose(run, wave_shift_up(incl, lane));
+    if (j < segments) {
+      double* fj = st + j * kLongStateDoubles + 12;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) fj[i] = f.m[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) fj[9 + i] = f.v[i];
+    }
+    Rigid<double> chunk;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) chunk.m[i] = __shfl(incl.m[i], 63);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) chunk.v[i] = __shfl(incl.v[i], 63);
+    run = compose(run, chunk);
   }
 }
 
@@ -175,33 +196,46 @@ __global__ __launch_bounds__(kLongThreads) void long_backward_sums_kernel(const 
   }
 }
 
-// One thread per chain: the suffix carry of every segment, last to first, each moved to its
-// segment's x2 (M about a = M about b + (b - a) x F).
+// One wave per chain: the suffix carry of every segment.  With moments taken about the
+// world origin (W = M + x2 x F for a segment's own sums), the carry of segment j is
+// F = sum_{l>j} F_l and M = sum_{l>j} W_l - x2_j x F: an exclusive suffix sum over segments,
+// lane l holding segment 64c + l, chunks from the last.
 __global__ __launch_bounds__(kLongThreads) void long_backward_carry_kernel(const double* __restrict__ state,
                                                                           double* __restrict__ work, int64_t batch,
                                                                           int segments) {
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * kLongThreads + threadIdx.x;
-  if (b >= batch) return;
-  double F[3] = {0, 0, 0}, M[3] = {0, 0, 0};
-  for (int j = segments - 1; j >= 0; --j) {
-    const int64_t at = b * segments + j;
-    double* w = work + at * kLongWorkDoubles;
-    for (int i = 0; i < 3; ++i) {
-      w[6 + i] = F[i];
-      w[9 + i] = M[i];
+  const int lane = threadIdx.x & 63;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * (kLongThreads / 64) + (threadIdx.x >> 6);
+  if (b >= batch) return;  // uniform per wave
+  const double* st = state + b * segments * kLongStateDoubles;
+  double* wk = work + b * segments * kLongWorkDoubles;
+  ForceMoment<double> later = {{0, 0, 0}, {0, 0, 0}};  // every chunk after this one
+  for (int c = (segments - 1) / 64; c >= 0; --c) {
+    const int j = 64 * c + lane;
+    ForceMoment<double> own = {{0, 0, 0}, {0, 0, 0}};
+    V3<double> o = {0, 0, 0};
+    if (j < segments) {
+      const double* x2 = st + j * kLongStateDoubles + 21;
+      o = {x2[0], x2[1], x2[2]};
+      if (j >= 1) {  // the head's own sums are never needed
+        const double* w = wk + j * kLongWorkDoubles;
+        own.f = {w[0], w[1], w[2]};
+        own.m = V3<double>{w[3], w[4], w[5]} + cross(o, own.f);
+      }
     }
-    if (j == 0) break;
-    // Add segment j's own sums, then move from x2 of segment j to x2 of segment j-1.
-    for (int i = 0; i < 3; ++i) {
-      F[i] += w[i];
-      M[i] += w[3 + i];
+    const ForceMoment<double> incl = wave_suffix(own, lane);
+    ForceMoment<double> after;  // lanes above this one, then the later chunks
+    after.f = V3<double>{shfl_down_or_zero(incl.f.x, 1, lane), shfl_down_or_zero(incl.f.y, 1, lane),
+                         shfl_down_or_zero(incl.f.z, 1, lane)} + later.f;
+    after.m = V3<double>{shfl_down_or_zero(incl.m.x, 1, lane), shfl_down_or_zero(incl.m.y, 1, lane),
+                         shfl_down_or_zero(incl.m.z, 1, lane)} + later.m;
+    if (j < segments) {
+      double* w = wk + j * kLongWorkDoubles + 6;
+      const V3<double> m = after.m - cross(o, after.f);
+      w[0] = after.f.x; w[1] = after.f.y; w[2] = after.f.z;
+      w[3] = m.x; w[4] = m.y; w[5] = m.z;
     }
-    const double* oj = state + at * kLongStateDoubles + 21;
-    const double* op = state + (at - 1) * kLongStateDoubles + 21;
-    const double d[3] = {oj[0] - op[0], oj[1] - op[1], oj[2] - op[2]};
-    M[0] += d[1] * F[2] - d[2] * F[1];
-    M[1] += d[2] * F[0] - d[0] * F[2];
-    M[2] += d[0] * F[1] - d[1] * F[0];
+    later.f = later.f + V3<double>{__shfl(incl.f.x, 0), __shfl(incl.f.y, 0), __shfl(incl.f.z, 0)};
+    later.m = later.m + V3<double>{__shfl(incl.m.x, 0), __shfl(incl.m.y, 0), __shfl(incl.m.z, 0)};
   }
 }
 
