@@ -14,6 +14,7 @@
 
 #include "chain_ops.h"
 #include "long_chain_kernels.h"
+#include "packed_kernels.h"
 #include "reconstruct_kernels.h"
 #include "staging.h"
 #include "torsion_kernels.h"
@@ -66,11 +67,72 @@ template <typename Fn> int launch_chunks(int64_t batch, int threads, Fn&& fn) {
   return CUFK_OK;
 }
 
+// Short chains: G lanes per chain, 8 steps per lane, 64W/G chains per workgroup (packed
+// kernels).  Measured on MI355X against one chain per workgroup: packing wins from about 4096
+// chains up (at 8192 chains: forward 9.5-15.5 us against 19-21 us for 9-128 steps), loses
+// below (fewer waves in flight), and its backward stops winning past 64 steps (at 128 steps
+// and 32768 chains: 44 us against 34 us).
+constexpr int kPackedFwdMaxSteps = 128;
+constexpr int kPackedBwdMaxSteps = 64;
+constexpr int64_t kPackedMinBatch = 4096;
+constexpr int kPackedWaves = 2;
+template <int MaxG = 16, typename Fn> int with_packed_plan(int steps, Fn&& fn) {
+  if (steps <= 8) return fn.template operator()<1>();
+  if (steps <= 16) return fn.template operator()<2>();
+  if (steps <= 32) return fn.template operator()<4>();
+  if (MaxG == 8 || steps <= 64) return fn.template operator()<8>();
+  if constexpr (MaxG >= 16) return fn.template operator()<16>();
+  return CUFK_ERR_STEPS;
+}
+inline bool use_packed_fwd(int64_t B, int steps) { return steps <= kPackedFwdMaxSteps && B >= kPackedMinBatch; }
+inline bool use_packed_bwd(int64_t B, int steps) { return steps <= kPackedBwdMaxSteps && B >= kPackedMinBatch; }
+// Launch a packed kernel over B chains, C per workgroup, in grid chunks that keep the grid's
+// work-item count within 32 bits.
+template <typename Fn> int launch_packed(int64_t B, int C, Fn&& fn) {
+  const int64_t threads = 64 * kPackedWaves;
+  const int64_t chunk = (int64_t{UINT32_MAX} / threads) * C;
+  for (int64_t done = 0; done < B; done += chunk) {
+    const int64_t n = B - done < chunk ? B - done : chunk;
+    fn(done, n, static_cast<unsigned>((n + C - 1) / C));
+    if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
+  }
+  return CUFK_OK;
+}
+
+template <typename T>
+int packed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz,
+                     uint8_t* regular, int64_t B, int N, hipStream_t st) {
+  return with_packed_plan(N - 3, [&]<int G>() {
+    constexpr int C = 64 * kPackedWaves / G;
+    return launch_packed(B, C, [&](int64_t off, int64_t n, unsigned groups) {
+      hipLaunchKernelGGL((packed_forward_kernel<T, kPackedWaves, G, 8>), dim3(groups), dim3(64 * kPackedWaves), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
+                         regular ? regular + off : nullptr, n, N);
+    });
+  });
+}
+
+template <typename T, bool Saved>
+int packed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+  static_assert(kPackedBwdMaxSteps <= 64, "the packed backward is compiled for up to 8 lanes per chain");
+  return with_packed_plan<8>(N - 3, [&]<int G>() {
+    constexpr int C = 64 * kPackedWaves / G;
+    return launch_packed(B, C, [&](int64_t off, int64_t n, unsigned groups) {
+      hipLaunchKernelGGL((packed_backward_kernel<T, kPackedWaves, G, 8, Saved>), dim3(groups), dim3(64 * kPackedWaves),
+                         0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0,
+                         Saved ? xyz + off * N * 3 : nullptr, Saved ? regular + off : nullptr, g + off * N * 3,
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), n, N);
+    });
+  });
+}
+
 // ---------------------------------------------------------------------------- reconstruct
 
 template <typename T>
 int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz,
                           uint8_t* regular, int64_t B, int N, hipStream_t st) {
+  if (use_packed_fwd(B, N - 3)) return packed_fwd_typed<T>(L, A, D, p0, fd, n0, xyz, regular, B, N, st);
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st, L + off * (N - 1),
@@ -85,6 +147,8 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
 template <typename T>
 int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
                                     const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+  if (use_packed_bwd(B, N - 3))
+    return packed_bwd_typed<T, false>(L, A, D, p0, fd, n0, nullptr, nullptr, g, gL, gA, gD, B, N, st);
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_recompute_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
@@ -100,6 +164,8 @@ template <typename T>
 int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
                                 const T* xyz, const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N,
                                 hipStream_t st) {
+  if (use_packed_bwd(B, N - 3))
+    return packed_bwd_typed<T, true>(L, A, D, p0, fd, n0, xyz, regular, g, gL, gA, gD, B, N, st);
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
