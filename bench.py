@@ -24,7 +24,7 @@ The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host
 sample of chains of the same shape (chunks of about 128 x 2049 points until about 15 s of work),
 scaled to atoms/s.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long|short]
 """
 
 from __future__ import annotations
@@ -50,6 +50,8 @@ CONFIGS = {
     # Past the 2051-point cap (reconstruct_long): C2's atom count as 64 chains of 131075 points,
     # 64 segments of 2048 steps each.
     "long": ("long", "float32", 64, 131075),
+    # Short chains packed several per wave: C2's atom count as 131072 chains of 64 points.
+    "short": ("reconstruct", "float32", 131072, 64),
 }
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
