@@ -24,7 +24,7 @@ The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host
 sample of chains of the same shape (chunks of about 128 x 2049 points until about 15 s of work),
 scaled to atoms/s.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long|short]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss]
 """
 
 from __future__ import annotations
@@ -52,6 +52,9 @@ CONFIGS = {
     "long": ("long", "float32", 64, 131075),
     # Short chains packed several per wave: C2's atom count as 131072 chains of 64 points.
     "short": ("reconstruct", "float32", 131072, 64),
+    # reconstruct_loss (reconstruction fused with a per-chain coordinate loss) at C2's shape; the
+    # unfused composition (reconstruct, then the loss in torch) is timed beside it.
+    "loss": ("loss", "float32", 4096, 2049),
 }
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
@@ -239,6 +242,48 @@ def main():
             steps.append(step)
             fwds.append(fwd)
             bwds.append(bwd)
+    elif kind == "loss":
+        # Forward reads the parameters and the target and writes xyz (s(9N-6)); backward reads
+        # xyz and the target and writes the three gradient rows (s(9N-6)): grad_xyz never
+        # exists, and the loss terms never leave the kernels.
+        fwd_bytes = s * B * (9 * N - 6)
+        bwd_bytes = s * B * (9 * N - 6)
+        unfused = []
+        for k in range(nsets):
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype)
+            target = g * 0.3  # any (B, N, 3) tensor: the loss only shifts by a constant
+            for t in (L, A, D):
+                t.requires_grad_(True)
+
+            def step(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, mark=None):
+                loss = cufk_amd.reconstruct_loss(L, A, D, target, p0, fd, n0)
+                if mark is not None:
+                    mark.record()
+                return torch.autograd.grad(loss.sum(), (L, A, D))
+
+            def plain(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
+                xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
+                return torch.autograd.grad(((xyz - target) ** 2).sum(), (L, A, D))
+
+            loss_out = torch.empty(B, device=device, dtype=dtype)
+            xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+            flags = torch.empty(B, device=device, dtype=torch.uint8)
+            gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+
+            def fwd(st, L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, loss_out=loss_out):
+                rc = lib.cufk_reconstruct_loss_fwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(target), P(xyz),
+                                                   P(flags), P(loss_out), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            def bwd(st, L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, gL=gL, gA=gA, gD=gD):
+                rc = lib.cufk_reconstruct_loss_bwd(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(flags),
+                                                   P(target), None, P(gL), P(gA), P(gD), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            steps.append(step)
+            fwds.append(fwd)
+            bwds.append(bwd)
+            unfused.append(plain)
     elif kind == "reconstruct":
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
@@ -347,6 +392,19 @@ def main():
     t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), args.kernel_reps)
     regular_frac = float(torch.stack(regular).float().mean()) if regular else None
 
+    unfused_us = None
+    if kind == "loss":  # the same step through reconstruct and a torch loss, same input sets
+        for i in range(args.warmup // 4):
+            unfused[i % nsets]()
+        torch.cuda.synchronize()
+        u0, u1 = ev(), ev()
+        u0.record(stream)
+        for i in range(args.steps):
+            unfused[i % nsets]()
+        u1.record(stream)
+        torch.cuda.synchronize()
+        unfused_us = u0.elapsed_time(u1) / args.steps * 1e3
+
     atoms = B * N
     bw_bwd = bwd_bytes / (t_bwd * 1e-3) / 1e9
     bw_fwd = fwd_bytes / (t_fwd * 1e-3) / 1e9
@@ -386,6 +444,7 @@ def main():
             "abi_backward_GBs": bw_bwd,
             "step_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "regular_chain_fraction": regular_frac,
+            "unfused_step_us": unfused_us,
         },
     }
     if not args.no_cpu_baseline:

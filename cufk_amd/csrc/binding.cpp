@@ -207,6 +207,71 @@ Tensor apply_reconstruct(const Tensor& lengths, const Tensor& angles, const Tens
   return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
 }
 
+// ------------------------------------------------------------------ fused coordinate loss
+
+// loss[b] = sum_i |x_bi - target_bi|^2 with the reconstruction fused in (no reference
+// counterpart).  Gradients flow to lengths, angles and dihedrals; not to the target or anchors.
+class LossAutograd : public torch::autograd::Function<LossAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
+                        Tensor target, Tensor p0, Tensor first_direction, Tensor initial_normal) {
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    check_like(target, lengths, "target", true);
+    TORCH_CHECK(target.sizes() == torch::IntArrayRef({shape.batch, shape.points, 3}), "target must have shape (B, N, 3)");
+    TORCH_CHECK(!target.requires_grad(), "target gradients are not supported");
+    const c10::DeviceGuard guard(lengths.device());
+    check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
+    Tensor loss = torch::empty({shape.batch}, lengths.options());
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
+    check_status(cufk_reconstruct_loss_fwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                           dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                           a.initial_normal.data_ptr(), target.data_ptr(), xyz.data_ptr(),
+                                           static_cast<uint8_t*>(regular.data_ptr()), loss.data_ptr(), shape.batch,
+                                           shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_loss_fwd");
+    // The positions stay internal (never returned), so nothing can modify them before backward.
+    ctx->save_for_backward({lengths, angles, dihedrals, target, a.p0, a.first_direction, a.initial_normal});
+    ctx->saved_data["xyz"] = xyz;
+    ctx->saved_data["regular"] = regular;
+    return loss;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& lengths = saved[0];
+    const Tensor& angles = saved[1];
+    const Tensor& dihedrals = saved[2];
+    const Tensor& target = saved[3];
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true);
+    Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_loss, lengths, "grad_loss", true);
+    const c10::DeviceGuard guard(lengths.device());
+    Tensor grad_lengths = torch::empty_like(lengths);
+    Tensor grad_angles = torch::empty_like(angles);
+    Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    const Tensor regular = ctx->saved_data["regular"].toTensor();
+    check_status(cufk_reconstruct_loss_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                           dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                           a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                           static_cast<const uint8_t*>(regular.data_ptr()), target.data_ptr(),
+                                           grad_loss.data_ptr(),
+                                           grad_lengths.data_ptr(), grad_angles.data_ptr(), grad_dihedrals.data_ptr(),
+                                           shape.batch, shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_loss_bwd");
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
+  }
+};
+
+Tensor apply_loss(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& target,
+                  const Tensor& p0, const Tensor& first_direction, const Tensor& initial_normal) {
+  return LossAutograd::apply(lengths, angles, dihedrals, target, p0, first_direction, initial_normal);
+}
+
 // ------------------------------------------------------------------ long chains
 
 // Segmented reconstruction without the 2048-step cap (no reference counterpart: its README:58
@@ -391,6 +456,9 @@ std::vector<int64_t> validate_torsion(const Tensor& raw_pairs, bool device) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("apply", &apply_reconstruct, "reconstruct autograd apply (block.cu:443-445)", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
+  m.def("apply_loss", &apply_loss, "fused reconstruct + per-chain coordinate loss", py::arg("lengths"),
+        py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"), py::arg("first_direction"),
+        py::arg("initial_normal"));
   m.def("apply_long", &apply_reconstruct_long, "segmented reconstruct for chains of any length", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"),
         py::arg("segment_steps") = 0);

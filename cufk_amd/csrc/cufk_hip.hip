@@ -175,6 +175,33 @@ int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0,
   });
 }
 
+// Fused coordinate loss: one workgroup per chain, the plans of the reconstruct kernels.
+template <typename T>
+int loss_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target, T* xyz,
+                   uint8_t* regular, T* loss, int64_t B, int N, hipStream_t st) {
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_loss_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, target + off * N * 3,
+                         xyz + off * N * 3, regular + off, loss + off, N);
+    });
+  });
+}
+
+template <typename T>
+int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                   const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
+                   hipStream_t st) {
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
+                         regular + off, target + off * N * 3, grad_loss != nullptr ? grad_loss + off : nullptr,
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+    });
+  });
+}
+
 // ---------------------------------------------------------------------------- long chains
 
 // Default segment length: the largest plan capacity (2048 steps) unless the grid would then
@@ -406,6 +433,46 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
   return dispatch(dtype, [&]<typename T>() {
     return torsion_bwd_typed<T>(cp<T>(raw_pairs), raw_stride, cp<T>(xyz), cp<T>(grad_xyz), mp<T>(grad_raw),
                                 grad_raw_stride, args, batch, N, st);
+  });
+}
+
+int cufk_reconstruct_loss_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal,
+                              const void* target, void* xyz, uint8_t* chain_regular, void* loss, int64_t batch,
+                              int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !target || !xyz ||
+      !chain_regular || !loss)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return loss_fwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                             cp<T>(initial_normal), cp<T>(target), mp<T>(xyz), chain_regular, mp<T>(loss), batch,
+                             static_cast<int>(points), st);
+  });
+}
+
+int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, const void* xyz,
+                              const uint8_t* chain_regular, const void* target, const void* grad_loss,
+                              void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                              int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !xyz || !chain_regular ||
+      !target || !grad_lengths || !grad_angles || !grad_dihedrals)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return loss_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                             cp<T>(initial_normal), cp<T>(xyz), chain_regular, cp<T>(target), cp<T>(grad_loss),
+                             mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch,
+                             static_cast<int>(points), st);
   });
 }
 

@@ -74,13 +74,17 @@ __device__ __forceinline__ void store_total(double* __restrict__ total, const Ri
 // points in the frame of the segment start (x2 of the view) and leave points 0..2 alone.
 // Every segment writes its total transform (row-major rotation, then translation; double) to
 // total[0..11].
-template <typename T, typename Lay, bool Segmented>
+//
+// Loss: *loss also receives sum_i |x_i - target_i|^2 over the chain's points (target: the
+// chain's (points, 3) row), from the positions as stored (rounded to T), accumulated in double.
+template <typename T, typename Lay, bool Segmented, bool Loss = false>
 __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                               const T* __restrict__ Dr, const T* __restrict__ p0,
                                               const T* __restrict__ first_direction,
                                               const T* __restrict__ initial_normal, T* __restrict__ out,
                                               uint8_t* __restrict__ regular, int points, bool head,
-                                              double* __restrict__ total) {
+                                              double* __restrict__ total, const T* __restrict__ target = nullptr,
+                                              T* __restrict__ loss = nullptr) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -106,6 +110,9 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
   if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid);
+  // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
+  R tr[Loss ? 3 * K : 1];
+  if constexpr (Loss) load_run<3 * K>(target + 9 + 3 * s0, count > 0 ? 3 * count : 0, tr);
   FirstFrame<R> ff;
   if (wave == 0) {
     if (!Segmented || head) {
@@ -181,12 +188,18 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
 
   R xmax = R(0);
+  double acc = 0.0;  // Loss: this thread's share of sum |x - target|^2
   {
     const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
       if (i < count) {
         const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+        if constexpr (Loss) {
+          const V3<R> xs = {widen(narrow<T>(x.x)), widen(narrow<T>(x.y)), widen(narrow<T>(x.z))};
+          const V3<R> d = xs - V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]};
+          acc += static_cast<double>(dot(d, d));
+        }
         stage[o0 + 3 * i] = x.x;
         stage[o0 + 3 * i + 1] = x.y;
         stage[o0 + 3 * i + 2] = x.z;
@@ -194,6 +207,15 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       }
     }
     if (tid == 0 && (!Segmented || head)) {
+      if constexpr (Loss) {
+        const V3<R> h[3] = {ff.p0, ff.p1, ff.p2};
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const V3<R> xs = {widen(narrow<T>(h[j].x)), widen(narrow<T>(h[j].y)), widen(narrow<T>(h[j].z))};
+          const V3<R> d = xs - V3<R>{widen(target[3 * j]), widen(target[3 * j + 1]), widen(target[3 * j + 2])};
+          acc += static_cast<double>(dot(d, d));
+        }
+      }
       stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
       stage[3] = ff.p1.x; stage[4] = ff.p1.y; stage[5] = ff.p1.z;
       stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
@@ -228,6 +250,19 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     }
     *regular = reg ? 1 : 0;
   }
+  if constexpr (Loss) {
+    __shared__ double loss_part[W];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d);
+    if (lane == 0) loss_part[wave] = acc;
+    __syncthreads();
+    if (tid == 0) {
+      double sum = 0.0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) sum += loss_part[w];
+      *loss = narrow<T>(static_cast<R>(sum));
+    }
+  }
   store_point_row<Lay>(out, stage, points, tid, !Segmented || head);
 }
 
@@ -259,7 +294,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
 // than the first (head) starts from the world rotation frame[0..8] (row-major) at its x2,
 // and carry[0..5] holds F and M (about that x2) of every point after the segment; only the
 // head writes the first-frame terms.
-template <typename T, typename Lay, bool Segmented = false>
+template <typename T, typename Lay, bool Segmented = false, bool StageGrad = true>
 __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                             const T* __restrict__ Dr, const T* __restrict__ p0,
                                             const T* __restrict__ first_direction,
@@ -285,9 +320,11 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
     R* const dst[3] = {pstage, pstage + Lay::kStepRow, pstage + 2 * Lay::kStepRow};
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
-    R* const gdst[1] = {gstage};
-    const T* const gsrc[1] = {Gr};
-    load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
+    if constexpr (StageGrad) {  // otherwise the caller left the gradient row in gstage
+      R* const gdst[1] = {gstage};
+      const T* const gsrc[1] = {Gr};
+      load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
+    }
   }
   FirstFrame<R> ff;
   R Fm[9];  // world rotation at x2
@@ -726,6 +763,69 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
     exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                         first_direction, initial_normal, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a,
                         region_b, wave_total, wave_sum, wide_vote, points);
+  }
+}
+
+// ============================================================================ fused coordinate loss
+
+// Forward of sum_i |x_i - target_i|^2 per chain: the flagged forward (positions and the
+// regularity flag written as reconstruct_forward_kernel writes them) with the loss reduced in
+// the workgroup from the positions in registers.
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_loss_forward_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ target, T* __restrict__ xyz, uint8_t* __restrict__ regular, T* __restrict__ loss,
+    int points) {
+  const int64_t row = blockIdx.x;
+  forward_chain<T, Layout<W, K, Pad>, false, true>(lengths + row * (points - 1), angles + row * (points - 2),
+                                                   dihedrals + row * (points - 3), p0, first_direction, initial_normal,
+                                                   xyz + row * points * 3, regular + row, points, true, nullptr,
+                                                   target + row * points * 3, loss + row);
+}
+
+// Its backward over the saved positions: the gradient row 2 w_b (x - target) is formed in LDS
+// from the staged positions and target (grad_xyz never exists in HBM), then the
+// position-based adjoint for regular chains and the exact one for the others, as in
+// reconstruct_backward_saved_kernel.
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ target,
+    const T* __restrict__ grad_loss, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
+    T* __restrict__ grad_dihedrals, int points) {
+  using R = compute_t<T>;
+  using Lay = Layout<W, K, Pad>;
+  constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R region_a[kA];
+  __shared__ __align__(16) R region_b[Lay::kPointRow];
+  __shared__ R wave_total[W][12];
+  __shared__ R wave_sum[W][6];
+  __shared__ int wide_vote[W];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  {
+    R* const dst[2] = {region_a, region_b};
+    const T* const src[2] = {xyz + row * points * 3, target + row * points * 3};
+    load_point_rows<Lay, 2>(dst, src, points, tid);
+  }
+  __syncthreads();
+  const R w2 = R(2) * (grad_loss != nullptr ? widen(grad_loss[row]) : R(1));
+  for (int e = tid; e < 3 * points; e += Lay::kLanes) {
+    const int slot = Lay::point_slot(e);
+    region_b[slot] = w2 * (region_a[slot] - region_b[slot]);
+  }
+  __syncthreads();
+  T* gLr = grad_lengths + row * (points - 1);
+  T* gAr = grad_angles + row * (points - 2);
+  T* gDr = grad_dihedrals + row * (points - 3);
+  if (FastPath<T>::kEnabled && regular[row] != 0) {
+    position_adjoint<T, Lay>(gLr, gAr, gDr, region_a, region_b, wave_sum, points);
+  } else {
+    exact_chain<T, Lay, false, false>(lengths + row * (points - 1), angles + row * (points - 2),
+                                      dihedrals + row * (points - 3), p0, first_direction, initial_normal, nullptr, gLr,
+                                      gAr, gDr, region_a, region_b, wave_total, wave_sum, wide_vote, points);
   }
 }
 

@@ -111,3 +111,46 @@ def reconstruct_long(
         0 if segment_steps is None else int(segment_steps),
     )
     return xyz[0] if single else xyz
+
+
+def reconstruct_loss(
+    lengths: torch.Tensor,
+    angles: torch.Tensor,
+    dihedrals: torch.Tensor,
+    target: torch.Tensor,
+    p0: torch.Tensor | None = None,
+    first_direction: torch.Tensor | None = None,
+    initial_normal: torch.Tensor | None = None,
+) -> torch.Tensor:
+    r"""Per-chain coordinate loss :math:`\sum_i \lVert x_i - t_i \rVert^2` of the reconstruction,
+    fused with it.
+
+    Equal to ``((reconstruct(lengths, angles, dihedrals, ...) - target) ** 2).sum((-2, -1))``,
+    but the coordinates never reach memory: the forward returns only the loss, and the
+    backward recomputes the positions and forms their gradient inside the kernel.
+
+    Args:
+        lengths, angles, dihedrals, p0, first_direction, initial_normal: as for
+            :func:`reconstruct` (4 <= N <= 2051).
+        target: ``(N, 3)`` or ``(B, N, 3)``, dtype and device of ``lengths``; no gradient.
+
+    Returns:
+        ``(B,)`` losses, or a 0-d tensor for one chain.  Gradients flow to lengths, angles and
+        dihedrals.  The reference has no counterpart (it leaves the loss to PyTorch).
+    """
+    lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
+    if single:
+        target = target[None]
+    p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
+    first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
+    initial_normal = _anchor(initial_normal, (0.0, 0.0, 1.0), lengths)
+    loss = _C.apply_loss(
+        lengths.contiguous(),
+        angles.contiguous(),
+        dihedrals.contiguous(),
+        target.contiguous(),
+        p0,
+        first_direction,
+        initial_normal,
+    )
+    return loss[0] if single else loss

@@ -123,6 +123,28 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
                      int64_t points, void* stream);
 
 /*
+ * Fused coordinate loss: loss[b] = sum_i |x_bi - target_bi|^2 over the points of chain b, with
+ * x the reconstruction of (lengths, angles, dihedrals, anchors); target is (B, N, 3) in the
+ * same dtype, loss (B,).  No reference counterpart: the reference reconstructs
+ * (block.cu:319-329) and leaves the loss to PyTorch, whose kernels read xyz and the target,
+ * write and read back the loss terms and grad_xyz, and hand grad_xyz to its backward
+ * (block.cu:331-365).  Here the forward writes xyz and chain_regular exactly as
+ * cufk_reconstruct_fwd_flagged does, plus the loss reduced from the positions in registers;
+ * the backward reads xyz and the target and forms grad_xyz = 2 grad_loss[b] (x - target) in
+ * LDS, so grad_xyz never exists in memory.  The loss uses the positions as stored (rounded to
+ * the dtype).  grad_loss (B,) may be NULL (all ones).  4 <= N <= 2051.
+ */
+int cufk_reconstruct_loss_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal,
+                              const void* target, void* xyz, uint8_t* chain_regular, void* loss, int64_t batch,
+                              int64_t points, void* stream);
+int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                              const void* p0, const void* first_direction, const void* initial_normal, const void* xyz,
+                              const uint8_t* chain_regular, const void* target, const void* grad_loss,
+                              void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                              int64_t points, void* stream);
+
+/*
  * Long chains (any N >= 4; no step cap).  The reference stops at 2048 local transforms
  * (extension_utils.cuh:128-130) and its README:58 points long chains to a separate repository
  * (coord_scan_repro, not part of it), so these have no reference counterpart; they extend

@@ -27,6 +27,8 @@ def lib():
     lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
+    lib.cufk_reconstruct_loss_fwd.argtypes = [ctypes.c_int] + [vp] * 10 + [i64, i64, vp]
+    lib.cufk_reconstruct_loss_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, vp]
     lib.cufk_reconstruct_long_fwd.argtypes = [ctypes.c_int] + [vp] * 8 + [i64, i64, i64, vp]
     lib.cufk_reconstruct_long_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, i64, vp]
     for name in ("cufk_long_state_doubles", "cufk_long_work_doubles"):
@@ -57,6 +59,8 @@ def test_header_declares_the_entry_points():
         "cufk_reconstruct_fwd_flagged",
         "cufk_reconstruct_long_bwd",
         "cufk_reconstruct_long_fwd",
+        "cufk_reconstruct_loss_bwd",
+        "cufk_reconstruct_loss_fwd",
         "cufk_torsion_bwd",
         "cufk_torsion_fwd",
         "cufk_version",
@@ -158,3 +162,18 @@ def test_long_status_paths(lib):
     assert b(0, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 10, 0, null) == ERR_SEGMENT
     assert b(0, p, p, p, p, p, p, p, p, p, p, p, p, p, 0, 10, 4, null) == OK
     assert lib.cufk_error_string(ERR_SEGMENT) == b"segment length must be in [1, 2048] local transforms"
+
+
+def test_loss_status_paths(lib):
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_loss_fwd
+    assert f(9, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(0, p, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert f(0, p, p, p, p, p, p, null, p, p, p, 4, 10, null) == ERR_NULL  # target is required
+    assert f(0, p, p, p, p, p, p, p, p, null, p, 4, 10, null) == ERR_NULL  # flags are written
+    assert f(0, p, p, p, p, p, p, p, p, p, p, 0, 10, null) == OK
+    b = lib.cufk_reconstruct_loss_bwd
+    assert b(0, p, p, p, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL  # gradients are required
+    assert b(0, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 3, null) == ERR_POINTS  # grad_loss may be null
+    assert b(0, p, p, p, p, p, p, p, p, p, null, p, p, p, 0, 10, null) == OK
