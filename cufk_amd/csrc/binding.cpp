@@ -10,6 +10,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <array>
 #include <cstdint>
 #include <string>
@@ -106,8 +107,17 @@ struct Anchors {
   Tensor p0, first_direction, initial_normal;
 };
 
-// extension_utils.cuh:90-103.
-Anchors checked_anchors(const Tensor& p0, const Tensor& fd, const Tensor& n0, const Tensor& ref, bool device) {
+// extension_utils.cuh:90-103.  With allow_grad the anchors may require grad (the anchored
+// autograd below, which has no reference counterpart).
+Anchors checked_anchors(const Tensor& p0, const Tensor& fd, const Tensor& n0, const Tensor& ref, bool device,
+                        bool allow_grad = false) {
+  if (allow_grad) {
+    const Tensor d0 = p0.detach(), d1 = fd.detach(), d2 = n0.detach();
+    check_anchor(d0, ref, "p0", device);
+    check_anchor(d1, ref, "first_direction", device);
+    check_anchor(d2, ref, "initial_normal", device);
+    return {d0.contiguous(), d1.contiguous(), d2.contiguous()};
+  }
   check_anchor(p0, ref, "p0", device);
   check_anchor(fd, ref, "first_direction", device);
   check_anchor(n0, ref, "initial_normal", device);
@@ -205,6 +215,70 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
 Tensor apply_reconstruct(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
                          const Tensor& first_direction, const Tensor& initial_normal) {
   return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
+}
+
+// ------------------------------------------------------------------ anchor gradients
+
+// ReconstructAutograd with gradients for the anchors as well (no reference counterpart).
+class AnchoredAutograd : public torch::autograd::Function<AnchoredAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
+                        Tensor p0, Tensor first_direction, Tensor initial_normal) {
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true, true);
+    const c10::DeviceGuard guard(lengths.device());
+    check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
+    check_status(cufk_reconstruct_fwd_flagged(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                              dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                              a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                              static_cast<uint8_t*>(regular.data_ptr()), shape.batch, shape.points,
+                                              current_stream(lengths)),
+                 "cufk_reconstruct_fwd_flagged");
+    ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
+    ctx->saved_data["xyz"] = xyz.detach();
+    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["regular"] = regular;
+    return xyz;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& lengths = saved[0];
+    const Tensor& angles = saved[1];
+    const Tensor& dihedrals = saved[2];
+    Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_points, lengths, "grad_points", true);
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true, true);
+    const c10::DeviceGuard guard(lengths.device());
+    Tensor grad_lengths = torch::empty_like(lengths);
+    Tensor grad_angles = torch::empty_like(angles);
+    Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    Tensor grad_p0 = torch::empty({3}, lengths.options());
+    Tensor grad_fd = torch::empty({3}, lengths.options());
+    Tensor grad_n0 = torch::empty({3}, lengths.options());
+    Tensor work = torch::empty({std::max<int64_t>(shape.batch, 1) * 6}, lengths.options().dtype(torch::kFloat64));
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    const Tensor regular = ctx->saved_data["regular"].toTensor();
+    const bool unmodified = xyz._version() == ctx->saved_data["xyz_version"].toInt();
+    check_status(cufk_reconstruct_bwd_anchored(
+                     dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(),
+                     a.first_direction.data_ptr(), a.initial_normal.data_ptr(), unmodified ? xyz.data_ptr() : nullptr,
+                     unmodified ? static_cast<const uint8_t*>(regular.data_ptr()) : nullptr, grad_points.data_ptr(),
+                     grad_lengths.data_ptr(), grad_angles.data_ptr(), grad_dihedrals.data_ptr(),
+                     static_cast<double*>(work.data_ptr()), grad_p0.data_ptr(), grad_fd.data_ptr(), grad_n0.data_ptr(),
+                     shape.batch, shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_bwd_anchored");
+    return {grad_lengths, grad_angles, grad_dihedrals, grad_p0, grad_fd, grad_n0};
+  }
+};
+
+Tensor apply_anchored(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
+                      const Tensor& first_direction, const Tensor& initial_normal) {
+  return AnchoredAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
 }
 
 // ------------------------------------------------------------------ fused coordinate loss
@@ -456,6 +530,8 @@ std::vector<int64_t> validate_torsion(const Tensor& raw_pairs, bool device) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("apply", &apply_reconstruct, "reconstruct autograd apply (block.cu:443-445)", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
+  m.def("apply_anchored", &apply_anchored, "reconstruct with anchor gradients", py::arg("lengths"), py::arg("angles"),
+        py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
   m.def("apply_loss", &apply_loss, "fused reconstruct + per-chain coordinate loss", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"), py::arg("first_direction"),
         py::arg("initial_normal"));

@@ -114,7 +114,8 @@ int packed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* f
 
 template <typename T, bool Saved>
 int packed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
-                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st,
+                     double* anchor = nullptr) {
   static_assert(kPackedBwdMaxSteps <= 64, "the packed backward is compiled for up to 8 lanes per chain");
   return with_packed_plan<8>(N - 3, [&]<int G>() {
     constexpr int C = 64 * kPackedWaves / G;
@@ -122,7 +123,8 @@ int packed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* f
       hipLaunchKernelGGL((packed_backward_kernel<T, kPackedWaves, G, 8, Saved>), dim3(groups), dim3(64 * kPackedWaves),
                          0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0,
                          Saved ? xyz + off * N * 3 : nullptr, Saved ? regular + off : nullptr, g + off * N * 3,
-                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), n, N);
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), n, N,
+                         anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
 }
@@ -146,14 +148,16 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
 // position-based adjoint (or the exact one for irregular chains).
 template <typename T>
 int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
-                                    const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+                                    const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st,
+                                    double* anchor = nullptr) {
   if (use_packed_bwd(B, N - 3))
-    return packed_bwd_typed<T, false>(L, A, D, p0, fd, n0, nullptr, nullptr, g, gL, gA, gD, B, N, st);
+    return packed_bwd_typed<T, false>(L, A, D, p0, fd, n0, nullptr, nullptr, g, gL, gA, gD, B, N, st, anchor);
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_recompute_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, g + off * N * 3,
-                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
+                         anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
 }
@@ -163,14 +167,15 @@ int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T*
 template <typename T>
 int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
                                 const T* xyz, const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N,
-                                hipStream_t st) {
+                                hipStream_t st, double* anchor = nullptr) {
   if (use_packed_bwd(B, N - 3))
-    return packed_bwd_typed<T, true>(L, A, D, p0, fd, n0, xyz, regular, g, gL, gA, gD, B, N, st);
+    return packed_bwd_typed<T, true>(L, A, D, p0, fd, n0, xyz, regular, g, gL, gA, gD, B, N, st, anchor);
   return with_scan_plan(N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
-                         regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+                         regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
+                         anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
 }
@@ -433,6 +438,45 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
   return dispatch(dtype, [&]<typename T>() {
     return torsion_bwd_typed<T>(cp<T>(raw_pairs), raw_stride, cp<T>(xyz), cp<T>(grad_xyz), mp<T>(grad_raw),
                                 grad_raw_stride, args, batch, N, st);
+  });
+}
+
+int cufk_reconstruct_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                  const void* p0, const void* first_direction, const void* initial_normal,
+                                  const void* xyz, const uint8_t* chain_regular, const void* grad_xyz,
+                                  void* grad_lengths, void* grad_angles, void* grad_dihedrals, double* anchor_work,
+                                  void* grad_p0, void* grad_first_direction, void* grad_initial_normal, int64_t batch,
+                                  int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (!p0 || !first_direction || !initial_normal || !grad_p0 || !grad_first_direction || !grad_initial_normal)
+    return CUFK_ERR_NULL;
+  if (batch > 0 && (!lengths || !angles || !dihedrals || (xyz && !chain_regular) || !grad_xyz || !grad_lengths ||
+                    !grad_angles || !grad_dihedrals || !anchor_work))
+    return CUFK_ERR_NULL;
+  const int N = static_cast<int>(points);
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    int r = CUFK_OK;
+    if (batch > 0) {
+      if (xyz != nullptr && FastPath<T>::kEnabled) {
+        r = reconstruct_bwd_saved_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                           cp<T>(first_direction), cp<T>(initial_normal), cp<T>(xyz), chain_regular,
+                                           cp<T>(grad_xyz), mp<T>(grad_lengths), mp<T>(grad_angles),
+                                           mp<T>(grad_dihedrals), batch, N, st, anchor_work);
+      } else {
+        r = reconstruct_bwd_recompute_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                               cp<T>(first_direction), cp<T>(initial_normal), cp<T>(grad_xyz),
+                                               mp<T>(grad_lengths), mp<T>(grad_angles), mp<T>(grad_dihedrals), batch,
+                                               N, st, anchor_work);
+      }
+      if (r != CUFK_OK) return r;
+    }
+    hipLaunchKernelGGL(anchor_gradients_kernel<T>, dim3(1), dim3(kAnchorThreads), 0, st, anchor_work, batch,
+                       cp<T>(first_direction), cp<T>(initial_normal), mp<T>(grad_p0), mp<T>(grad_first_direction),
+                       mp<T>(grad_initial_normal));
+    return hipGetLastError() == hipSuccess ? int{CUFK_OK} : int{CUFK_ERR_LAUNCH};
   });
 }
 

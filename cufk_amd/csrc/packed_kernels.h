@@ -395,7 +395,7 @@ template <typename R, int K> struct LaneGrads {
 template <typename T, typename P, int G, int K>
 __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, const compute_t<T>* gs,
                                                         const PackedLane<G, K>& ln, int points, int lane,
-                                                        LaneGrads<compute_t<T>, K>& out) {
+                                                        LaneGrads<compute_t<T>, K>& out, double* anchor) {
   using R = compute_t<T>;
   const int last = ln.count - 1;
   const int e0 = ln.c * 3 * points + 3 * ln.s0;  // point s0: the three points before the lane's run, then the run
@@ -441,6 +441,10 @@ __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, 
     const int eg = ln.c * 3 * points;
     const V3<R> g1 = {gs[fslot<P::kPointGap>(eg + 3)], gs[fslot<P::kPointGap>(eg + 4)], gs[fslot<P::kPointGap>(eg + 5)]};
     const V3<R> g2 = {gs[fslot<P::kPointGap>(eg + 6)], gs[fslot<P::kPointGap>(eg + 7)], gs[fslot<P::kPointGap>(eg + 8)]};
+    if (anchor != nullptr) {
+      const V3<R> g0 = {gs[fslot<P::kPointGap>(eg)], gs[fslot<P::kPointGap>(eg + 1)], gs[fslot<P::kPointGap>(eg + 2)]};
+      store_anchor_sums(anchor, F, M, x0, x1, g0, g1, g2);
+    }
     F = F + g2;
     const V3<R> Tq = M - cross(x1, F);
     const V3<R> b1 = x2 - x1;
@@ -458,7 +462,7 @@ template <typename T, typename P, int G, int K>
 __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_t<T>>& rows, const compute_t<T>* gs,
                                                      const compute_t<T>* base, const FirstFrame<compute_t<T>>& ff,
                                                      const PackedLane<G, K>& ln, int points, bool wide,
-                                                     LaneGrads<compute_t<T>, K>& out) {
+                                                     LaneGrads<compute_t<T>, K>& out, double* anchor) {
   using R = compute_t<T>;
   const int lane = threadIdx.x & 63;
   const int el = ln.c * (points - 1) + 2 + ln.s0;
@@ -566,6 +570,10 @@ __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_
     const V3<R> F2 = Fs + g2;
     const V3<R> x1 = ff.p1 - ff.p2;
     const V3<R> tau2 = Ms - cross(x1, F2);
+    if (anchor != nullptr) {
+      const V3<R> g0 = {gs[fslot<P::kPointGap>(e)], gs[fslot<P::kPointGap>(e + 1)], gs[fslot<P::kPointGap>(e + 2)]};
+      store_anchor_sums(anchor, Fs, Ms, ff.p0 - ff.p2, x1, g0, g1, g2);
+    }
     out.head[0] = dot(ff.d0, F2 + g1);
     out.head[1] = dot(ff.d1, F2);
     out.head[2] = -dot(cross(ff.d0, ff.t0), tau2);
@@ -583,7 +591,7 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
     T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int64_t batch,
-    int points) {
+    int points, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using P = Packed<W, G, K>;
   constexpr int C = P::kChains;
@@ -696,10 +704,11 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
   }
   __syncthreads();  // staged rows (and positions, base) visible
   LaneGrads<R, K> out;
+  double* const an = anchor != nullptr && ln.leader ? anchor + (b0 + ln.c) * 6 : nullptr;
   if (positions)
-    packed_position_adjoint<T, P, G, K>(region_a, region_b, ln, points, lane, out);
+    packed_position_adjoint<T, P, G, K>(region_a, region_b, ln, points, lane, out, an);
   else
-    packed_exact_adjoint<T, P, G, K>(rows, region_b, base, ff, ln, points, wide, out);
+    packed_exact_adjoint<T, P, G, K>(rows, region_b, base, ff, ln, points, wide, out, an);
   __syncthreads();  // every read of region_a retired: the outputs replace it
 
   // Outputs in output-row order: lengths (N-1 per chain), angles (N-2), dihedrals (N-3).

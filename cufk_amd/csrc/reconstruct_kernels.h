@@ -61,6 +61,23 @@ __device__ __forceinline__ void store_total(double* __restrict__ total, const Ri
   }
 }
 
+// Per-chain sums for the anchor gradients, written by the thread that computes the
+// first-frame terms: F = sum_i g_i over all points and tau = sum_i (x_i - p0) x g_i, from the
+// sums over points >= 3 the adjoint ends with (F3, and M3 about x2) and points 0..2 relative to
+// x2 (P0 = p0 - x2, P1 = x1 - x2, x2 itself at the origin).
+template <typename R>
+__device__ __forceinline__ void store_anchor_sums(double* __restrict__ out, V3<R> F3, V3<R> M3, V3<R> P0, V3<R> P1,
+                                                  V3<R> g0, V3<R> g1, V3<R> g2) {
+  const V3<R> f = F3 + g0 + g1 + g2;
+  const V3<R> tau = M3 - cross(P0, F3) + cross(P1 - P0, g1) - cross(P0, g2);
+  out[0] = f.x;
+  out[1] = f.y;
+  out[2] = f.z;
+  out[3] = tau.x;
+  out[4] = tau.y;
+  out[5] = tau.z;
+}
+
 // ============================================================================ forward
 
 // x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v, for one
@@ -304,7 +321,8 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
                                             compute_t<T> (&wave_total)[Lay::kWaves][12],
                                             compute_t<T> (&wave_sum)[Lay::kWaves][6], int (&wide_vote)[Lay::kWaves],
                                             int points, bool head = true, const double* __restrict__ frame = nullptr,
-                                            const double* __restrict__ carry = nullptr) {
+                                            const double* __restrict__ carry = nullptr,
+                                            double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -448,6 +466,7 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
     const V3<R> F2 = Fs + g2;
     const V3<R> x1 = ff.p1 - ff.p2;
     const V3<R> tau2 = Ms - cross(x1, F2);
+    if (anchor != nullptr) store_anchor_sums(anchor, Fs, Ms, ff.p0 - ff.p2, x1, load3(&gstage[0]), g1, g2);
     gLr[0] = narrow<T>(dot(ff.d0, F2 + g1));
     gLr[1] = narrow<T>(dot(ff.d1, F2));
     gAr[0] = narrow<T>(-dot(cross(ff.d0, ff.t0), tau2));
@@ -471,7 +490,8 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 template <typename T, typename Lay>
 __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                  compute_t<T>* xs, compute_t<T>* gs,
-                                                 compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
+                                                 compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
+                                                 double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -540,6 +560,7 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
     const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
     const V3<R> g1 = load3(&gs[3]);
     const V3<R> g2 = load3(&gs[6]);
+    if (anchor != nullptr) store_anchor_sums(anchor, F, M, x0, x1, load3(&gs[0]), g1, g2);
     F = F + g2;
     const V3<R> Tq = M - cross(x1, F);
     const V3<R> b1 = x2 - x1;
@@ -568,14 +589,15 @@ template <typename T, typename Lay>
 __device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T* __restrict__ Gr,
                                                T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                compute_t<T>* xs, compute_t<T>* gs,
-                                               compute_t<T> (&wave_sum)[Lay::kWaves][6], int points) {
+                                               compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
+                                               double* __restrict__ anchor = nullptr) {
   {
     compute_t<T>* const dst[2] = {xs, gs};
     const T* const src[2] = {Xr, Gr};
     load_point_rows<Lay, 2>(dst, src, points, threadIdx.x);
   }
   __syncthreads();
-  position_adjoint<T, Lay>(gLr, gAr, gDr, xs, gs, wave_sum, points);
+  position_adjoint<T, Lay>(gLr, gAr, gDr, xs, gs, wave_sum, points, anchor);
 }
 
 // ============================================================================ recompute backward
@@ -597,7 +619,7 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
                                                 compute_t<T> (&wave_total)[Lay::kWaves][12],
                                                 compute_t<T> (&wave_sum)[Lay::kWaves][6],
                                                 compute_t<T> (&wave_stat)[Lay::kWaves][3], int (&wide_vote)[Lay::kWaves],
-                                                int points) {
+                                                int points, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Fast = FastPath<R>;
   constexpr int W = Lay::kWaves;
@@ -704,10 +726,10 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
       pstage[6] = R(0); pstage[7] = R(0); pstage[8] = R(0);
     }
     __syncthreads();
-    position_adjoint<T, Lay>(gLr, gAr, gDr, pstage, gstage, wave_sum, points);
+    position_adjoint<T, Lay>(gLr, gAr, gDr, pstage, gstage, wave_sum, points, anchor);
   } else {
     exact_chain<T, Lay>(Lr, Ar, Dr, p0, first_direction, initial_normal, Gr, gLr, gAr, gDr, pstage, gstage, wave_total,
-                        wave_sum, wide_vote, points);
+                        wave_sum, wide_vote, points, true, nullptr, nullptr, anchor);
   }
 }
 
@@ -717,7 +739,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_recompute_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points) {
+    T* __restrict__ grad_dihedrals, int points, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
@@ -731,7 +753,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_recompute_kernel(
   recompute_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                           first_direction, initial_normal, grad_xyz + row * points * 3, grad_lengths + row * (points - 1),
                           grad_angles + row * (points - 2), grad_dihedrals + row * (points - 3), region_a, region_b,
-                          wave_total, wave_sum, wave_stat, wide_vote, points);
+                          wave_total, wave_sum, wave_stat, wide_vote, points,
+                          anchor != nullptr ? anchor + row * 6 : nullptr);
 }
 
 // Backward given the forward's own output: one workgroup per chain, the position-based
@@ -743,7 +766,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
-    T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points) {
+    T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points,
+    double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
@@ -753,17 +777,91 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
   __shared__ R wave_sum[W][6];
   __shared__ int wide_vote[W];
   const int64_t row = blockIdx.x;
+  double* const an = anchor != nullptr ? anchor + row * 6 : nullptr;
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
   T* gDr = grad_dihedrals + row * (points - 3);
   if (regular[row] != 0) {
     position_chain<T, Lay>(xyz + row * points * 3, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a, region_b,
-                           wave_sum, points);
+                           wave_sum, points, an);
   } else {
     exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                         first_direction, initial_normal, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a,
-                        region_b, wave_total, wave_sum, wide_vote, points);
+                        region_b, wave_total, wave_sum, wide_vote, points, true, nullptr, nullptr, an);
   }
+}
+
+// ============================================================================ anchor gradients
+
+// One workgroup: the per-chain sums (F, tau) of `part` reduced over the batch in double, then
+// mapped to the anchors (no reference counterpart; the map follows from every point being
+// p0 + Q c_i with Q = [d, t, n] the orthonormal first frame):
+//   dL/dp0 = F;  dL = dd . (tau x d) - (tau . d)(dn . t) for a rotation moving d by dd and n by
+//   dn, then the chain rule through the normalisation of first_direction and the Gram-Schmidt
+//   step (or the fixed-helper normal stable_perpendicular(d) when that step degenerates).
+constexpr int kAnchorThreads = 256;
+template <typename T>
+__global__ __launch_bounds__(kAnchorThreads) void anchor_gradients_kernel(
+    const double* __restrict__ part, int64_t batch, const T* __restrict__ first_direction,
+    const T* __restrict__ initial_normal, T* __restrict__ grad_p0, T* __restrict__ grad_first_direction,
+    T* __restrict__ grad_initial_normal) {
+  __shared__ double red[kAnchorThreads / 64][6];
+  double acc[6] = {0, 0, 0, 0, 0, 0};
+  for (int64_t b = threadIdx.x; b < batch; b += kAnchorThreads) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) acc[k] += part[b * 6 + k];
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    double v = acc[k];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    if (lane == 0) red[wave][k] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  double sum[6] = {0, 0, 0, 0, 0, 0};
+  for (int w = 0; w < kAnchorThreads / 64; ++w)
+    for (int k = 0; k < 6; ++k) sum[k] += red[w][k];
+  const V3<double> F = {sum[0], sum[1], sum[2]};
+  const V3<double> tau = {sum[3], sum[4], sum[5]};
+  using R = compute_t<T>;
+  // The branch is decided as first_frame decides it, in the compute precision.
+  bool degenerate;
+  {
+    const V3<R> dr = normalized(V3<R>{widen(first_direction[0]), widen(first_direction[1]), widen(first_direction[2])});
+    const V3<R> nr0 = {widen(initial_normal[0]), widen(initial_normal[1]), widen(initial_normal[2])};
+    const V3<R> nn = nr0 - dot(nr0, dr) * dr;
+    degenerate = dot(nn, nn) < static_cast<R>(1.0e-12f);
+  }
+  const V3<double> f0 = {widen(first_direction[0]), widen(first_direction[1]), widen(first_direction[2])};
+  const V3<double> n0 = {widen(initial_normal[0]), widen(initial_normal[1]), widen(initial_normal[2])};
+  const double dn = sqrt(fmax(dot(f0, f0), static_cast<double>(1.0e-12f)));
+  const V3<double> d = {f0.x / dn, f0.y / dn, f0.z / dn};
+  const V3<double> nr = n0 - dot(n0, d) * d;
+  V3<double> gfd, gn0;
+  if (degenerate) {  // n = stable_perpendicular(d)
+    const V3<double> h = fabs(d.x) >= 0.9 ? V3<double>{0, 1, 0} : V3<double>{1, 0, 0};
+    const V3<double> dh = cross(d, h);
+    const double dhn = sqrt(dot(dh, dh));
+    const V3<double> n = {dh.x / dhn, dh.y / dhn, dh.z / dhn};
+    const V3<double> t = cross(n, d);
+    const V3<double> v = cross(tau, d) - (dot(tau, d) / dhn) * cross(h, t);
+    const V3<double> vp = v - dot(v, d) * d;
+    gfd = {vp.x / dn, vp.y / dn, vp.z / dn};
+    gn0 = {0, 0, 0};
+  } else {
+    const double nn = sqrt(dot(nr, nr));
+    const V3<double> n = {nr.x / nn, nr.y / nn, nr.z / nn};
+    const V3<double> t = cross(n, d);
+    const V3<double> v = cross(tau, d) + (dot(tau, d) * dot(n0, d) / nn) * t;
+    gfd = {v.x / dn, v.y / dn, v.z / dn};
+    gn0 = (-dot(tau, d) / nn) * t;
+  }
+  const double out[9] = {F.x, F.y, F.z, gfd.x, gfd.y, gfd.z, gn0.x, gn0.y, gn0.z};
+  T* const dst[3] = {grad_p0, grad_first_direction, grad_initial_normal};
+  for (int k = 0; k < 9; ++k) dst[k / 3][k % 3] = narrow<T>(static_cast<R>(out[k]));
 }
 
 // ============================================================================ fused coordinate loss

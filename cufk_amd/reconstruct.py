@@ -41,6 +41,8 @@ def reconstruct(
     p0: torch.Tensor | None = None,
     first_direction: torch.Tensor | None = None,
     initial_normal: torch.Tensor | None = None,
+    *,
+    anchor_grads: bool = False,
 ) -> torch.Tensor:
     r"""Reconstruct Cartesian coordinates from full internal coordinates.
 
@@ -57,14 +59,18 @@ def reconstruct(
 
     All inputs are GPU tensors of one dtype (float16, bfloat16, float32 or float64),
     4 <= N <= 2051.  Gradients flow to lengths, angles and dihedrals; anchors must not
-    require grad.
+    require grad, as in the reference.  With ``anchor_grads=True`` (an extension, keyword
+    only) the anchors may require grad and receive gradients too (assuming
+    ``|first_direction| >= 1e-6``; an ``initial_normal`` parallel to ``first_direction`` gets
+    a zero gradient, the normal then coming from a fixed helper axis).
     """
     lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
     p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
     first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
     initial_normal = _anchor(initial_normal, (0.0, 0.0, 1.0), lengths)
 
-    xyz = _C.apply(
+    apply = _C.apply_anchored if anchor_grads else _C.apply
+    xyz = apply(
         lengths.contiguous(),
         angles.contiguous(),
         dihedrals.contiguous(),

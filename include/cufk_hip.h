@@ -123,6 +123,23 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
                      int64_t points, void* stream);
 
 /*
+ * Backward with anchor gradients.  No reference counterpart: the reference rejects anchors
+ * that require grad (extension_utils.cuh:81, "gradients are not supported").  Computes what
+ * cufk_reconstruct_bwd_saved (xyz and chain_regular given) or cufk_reconstruct_bwd (xyz NULL)
+ * computes, plus dL/dp0, dL/dfirst_direction, dL/dinitial_normal (3 values each, summed over
+ * the batch since the anchors are shared).  anchor_work: 6*B doubles of scratch (per-chain
+ * force and torque about p0), no initialisation needed.  The gradients assume
+ * |first_direction| >= 1e-6; with initial_normal parallel to first_direction the normal comes
+ * from the fixed helper axis and dL/dinitial_normal is 0.
+ */
+int cufk_reconstruct_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                  const void* p0, const void* first_direction, const void* initial_normal,
+                                  const void* xyz, const uint8_t* chain_regular, const void* grad_xyz,
+                                  void* grad_lengths, void* grad_angles, void* grad_dihedrals, double* anchor_work,
+                                  void* grad_p0, void* grad_first_direction, void* grad_initial_normal, int64_t batch,
+                                  int64_t points, void* stream);
+
+/*
  * Fused coordinate loss: loss[b] = sum_i |x_bi - target_bi|^2 over the points of chain b, with
  * x the reconstruction of (lengths, angles, dihedrals, anchors); target is (B, N, 3) in the
  * same dtype, loss (B,).  No reference counterpart: the reference reconstructs

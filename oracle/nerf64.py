@@ -23,6 +23,9 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
 * ``torsion_forward`` / ``torsion_backward``: against ``reconstruct_forward``
   with tiled constants and ``D = atan2(rs, rc)``, and the chain rule through
   the pair normalisation, and finite differences.
+* ``anchor_gradients``: central finite differences of ``reconstruct_forward``
+  in each anchor component, for generic anchors and the degenerate-normal
+  branch, and torch.autograd through the torch restatement with its anchors.
 * ``torsion_constants``: closed form (float rounding of lengths, float64
   ``math.sin``/``math.cos`` of the angles printed with ``.17g``).
 
@@ -329,6 +332,50 @@ def reconstruct_backward_frames(lengths, angles, dihedrals, grad_xyz, p0=None, f
 
 
 # ---------------------------------------------------------------- independent checks
+
+
+def anchor_gradients(lengths, angles, dihedrals, grad_xyz, p0=None, first_direction=None, initial_normal=None):
+    """Gradients of sum(grad_xyz * xyz) with respect to the three anchors, summed over the batch
+    (the anchors are shared).  No reference counterpart: the reference rejects anchors that
+    require grad (extension_utils.cuh:81).
+
+    Every point is p0 + Q c_i with Q = [d, t, n] the orthonormal frame of first_frame
+    (d = first_direction normalised, n its Gram-Schmidt normal, t = n x d) and c_i independent
+    of the anchors, because every step of block.cu:113-148 and the scan commutes with
+    rotations.  So dL/dp0 = F = sum g, and an infinitesimal rotation w of Q changes L by
+    w . tau, tau = sum (x - p0) x g.  Expressing w through d and n (w x d = dd, w x n = dn)
+    gives dL = dd . (tau x d) - (tau . d)(dn . t), then the chain rule through the
+    normalisation of first_direction and the Gram-Schmidt step (or, for the degenerate normal,
+    stable_perpendicular(d) with its fixed helper axis).  Assumes |first_direction| >= 1e-6.
+
+    Returns (grad_p0, grad_first_direction, grad_initial_normal), each (3,).
+    """
+    L, _ = _as_batch(lengths)
+    A, _ = _as_batch(angles)
+    D, _ = _as_batch(dihedrals)
+    g = np.asarray(grad_xyz, np.float64).reshape(L.shape[0], -1, 3)
+    p0, fd, n0 = _anchors(p0, first_direction, initial_normal)
+    x = reconstruct_forward(L, A, D, p0, fd, n0).reshape(g.shape)
+    F = g.sum(axis=(0, 1))
+    tau = np.cross(x - p0, g).sum(axis=(0, 1))
+    dnorm = math.sqrt(max(float(fd @ fd), K_EPS))
+    d = fd / dnorm
+    n_raw = n0 - float(n0 @ d) * d
+    if float(n_raw @ n_raw) < K_EPS:  # degenerate: n = stable_perpendicular(d)
+        h = np.array([0.0, 1.0, 0.0]) if abs(d[0]) >= 0.9 else np.array([1.0, 0.0, 0.0])
+        dh = np.cross(d, h)
+        n = dh / math.sqrt(max(float(dh @ dh), K_EPS))
+        t = np.cross(n, d)
+        v = np.cross(tau, d) - float(tau @ d) * np.cross(h, t) / math.sqrt(float(dh @ dh))
+        grad_fd = (v - float(v @ d) * d) / dnorm
+        grad_n0 = np.zeros(3)
+    else:
+        nn = math.sqrt(float(n_raw @ n_raw))
+        n = n_raw / nn
+        t = np.cross(n, d)
+        grad_fd = (np.cross(tau, d) + float(tau @ d) * float(n0 @ d) / nn * t) / dnorm
+        grad_n0 = -float(tau @ d) / nn * t
+    return F, grad_fd, grad_n0
 
 
 def nerf_serial(lengths, angles, dihedrals, p0=None, first_direction=None, initial_normal=None):

@@ -27,6 +27,7 @@ def lib():
     lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
+    lib.cufk_reconstruct_bwd_anchored.argtypes = [ctypes.c_int] + [vp] * 16 + [i64, i64, vp]
     lib.cufk_reconstruct_loss_fwd.argtypes = [ctypes.c_int] + [vp] * 10 + [i64, i64, vp]
     lib.cufk_reconstruct_loss_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, vp]
     lib.cufk_reconstruct_long_fwd.argtypes = [ctypes.c_int] + [vp] * 8 + [i64, i64, i64, vp]
@@ -54,6 +55,7 @@ def test_header_declares_the_entry_points():
         "cufk_long_work_doubles",
         "cufk_max_steps",
         "cufk_reconstruct_bwd",
+        "cufk_reconstruct_bwd_anchored",
         "cufk_reconstruct_bwd_saved",
         "cufk_reconstruct_fwd",
         "cufk_reconstruct_fwd_flagged",
@@ -177,3 +179,15 @@ def test_loss_status_paths(lib):
     assert b(0, p, p, p, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL  # gradients are required
     assert b(0, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 3, null) == ERR_POINTS  # grad_loss may be null
     assert b(0, p, p, p, p, p, p, p, p, p, null, p, p, p, 0, 10, null) == OK
+
+
+def test_anchored_status_paths(lib):
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_bwd_anchored
+    #        dtype L  A  D  p0 d0 n0 xyz flags g  gL gA gD work gp0 gd0 gn0
+    assert f(9, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert f(0, p, p, p, p, p, p, p, null, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_NULL  # xyz needs its flags
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 10, null) == ERR_NULL  # scratch is required
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL  # anchor gradients too

@@ -145,6 +145,76 @@ def test_backward_matches_finite_differences_with_anchors():
         assert np.abs(fd - grads[idx]).max() < 1e-7
 
 
+@pytest.mark.parametrize(
+    "fd,n0",
+    [
+        (None, None),  # random anchors from the seed
+        ([0.3, -1.7, 0.4], [2.0, 0.1, -0.5]),  # neither unit length nor orthogonal
+        ([0.0, 0.0, 2.0], [0.0, 0.0, -3.0]),  # parallel: degenerate normal, helper e_x
+        ([1.5, 0.2, 0.0], [3.0, 0.4, 0.0]),  # parallel with |d_x| >= 0.9: helper e_y
+    ],
+)
+def test_anchor_gradients_match_finite_differences(fd, n0):
+    d = o.synthetic_inputs(3, 12, seed=31, anchors=True)
+    if fd is not None:
+        d["first_direction"], d["initial_normal"] = np.array(fd, float), np.array(n0, float)
+    an = _anchors(d)
+    g = d["grad"]
+    got = o.anchor_gradients(d["lengths"], d["angles"], d["dihedrals"], g, **an)
+    # The degenerate branch holds while |n0 - (n0.d) d|^2 < 1e-12: steps small enough to stay
+    # in it, with the larger roundoff that brings.
+    degenerate = fd is not None and abs(np.dot(np.cross(fd, n0), np.cross(fd, n0))) < 1e-20
+    h, tol = (1e-8, 1e-5) if degenerate else (1e-6, 1e-6)
+    for key, want in zip(("p0", "first_direction", "initial_normal"), got):
+        num = np.zeros(3)
+        for j in range(3):
+            plus, minus = dict(an), dict(an)
+            plus[key] = an[key].copy()
+            minus[key] = an[key].copy()
+            plus[key][j] += h
+            minus[key][j] -= h
+            fp = np.sum(o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **plus) * g)
+            fm = np.sum(o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **minus) * g)
+            num[j] = (fp - fm) / (2 * h)
+        assert np.abs(num - want).max() < tol * max(1.0, np.abs(want).max()), (key, num, want)
+
+
+def test_anchor_gradients_match_torch_autograd():
+    """The torch restatement of the recurrence, started from first-frame points built in
+    torch from anchors that require grad."""
+    d = o.synthetic_inputs(2, 9, seed=33, anchors=True)
+    p0, fd, n0 = (torch.tensor(d[k], requires_grad=True) for k in ("p0", "first_direction", "initial_normal"))
+    L, A, D = (torch.tensor(d[k]) for k in ("lengths", "angles", "dihedrals"))
+    dd = fd / fd.norm()
+    nr = n0 - (n0 @ dd) * dd
+    nn = nr / nr.norm()
+    t = torch.linalg.cross(nn, dd)
+    xs = []
+    for b in range(L.shape[0]):
+        x1 = p0 + L[b, 0] * dd
+        dir1 = -torch.cos(A[b, 0]) * dd + torch.sin(A[b, 0]) * t
+        pts = [p0, x1, x1 + L[b, 1] * dir1]
+        for k in range(L.shape[1] - 2):  # classic NeRF placement, step k uses L[k+2], A[k+1], D[k]
+            a, bb, c = pts[-3], pts[-2], pts[-1]
+            bc = (c - bb) / (c - bb).norm()
+            nv = torch.linalg.cross(bb - a, bc)
+            nv = nv / nv.norm()
+            m = torch.stack([bc, torch.linalg.cross(nv, bc), nv], dim=1)
+            th, ph = A[b, k + 1], D[b, k]
+            loc = L[b, k + 2] * torch.stack([-torch.cos(th), torch.sin(th) * torch.cos(ph), torch.sin(th) * torch.sin(ph)])
+            pts.append(c + m @ loc)
+        xs.append(torch.stack(pts))
+    x = torch.stack(xs)
+    assert np.abs(x.detach().numpy() - o.reconstruct_forward(**{k: d[k] for k in ("lengths", "angles", "dihedrals")},
+                                                                 p0=d["p0"], first_direction=d["first_direction"],
+                                                                 initial_normal=d["initial_normal"])).max() < 1e-12
+    got_t = torch.autograd.grad(x, (p0, fd, n0), torch.tensor(d["grad"]))
+    got_o = o.anchor_gradients(d["lengths"], d["angles"], d["dihedrals"], d["grad"], p0=d["p0"],
+                               first_direction=d["first_direction"], initial_normal=d["initial_normal"])
+    for a, b in zip(got_t, got_o):
+        assert np.abs(a.numpy() - b).max() < 1e-11
+
+
 def test_adjoint_forms_agree():
     d = o.synthetic_inputs(3, 60, seed=7, anchors=True)
     args = (d["lengths"], d["angles"], d["dihedrals"], d["grad"])
