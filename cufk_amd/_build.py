@@ -5,7 +5,8 @@
 * ``_C.<abi>.so``: the PyTorch-ROCm extension (autograd wrappers + validation), plain C++
   compiled by ``g++`` against torch and linked to ``libcufk_hip.so`` through ``$ORIGIN``.
 
-Run ``python -m cufk_amd._build`` (or ``__graft_entry__.build()``).  Every call recompiles.
+Run ``python cufk_amd/_build.py`` (or ``__graft_entry__.build()``); it imports nothing from
+the package, whose ``__init__`` needs the extension this builds.  Every call recompiles.
 """
 
 from __future__ import annotations

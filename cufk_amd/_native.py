@@ -14,7 +14,7 @@ try:
     from . import _C  # noqa: F401
 except ImportError as exc:  # pragma: no cover - exercised only on a broken install
     raise ImportError(
-        f"cufk_amd native extension not built in {_PKG} ({exc}); run `python -m cufk_amd._build`"
+        f"cufk_amd native extension not built in {_PKG} ({exc}); run `python cufk_amd/_build.py`"
     ) from exc
 
 HIP_LIBRARY = _PKG / "libcufk_hip.so"
