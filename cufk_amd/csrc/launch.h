@@ -1,0 +1,94 @@
+// Interface between the C ABI (cufk_hip.hip) and the typed kernel launchers (launchers.hip).
+//
+// launchers.hip is compiled once per (dtype, kernel family): the device code of the library
+// then builds as independent translation units, in parallel.  This header declares the typed
+// launchers those units instantiate and the limits the C ABI checks against; it instantiates
+// no kernel itself.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "cufk_hip.h"
+#include "reconstruct_kernels.h"  // FastPath
+#include "torsion_kernels.h"      // TorsionArgs
+
+namespace cufk_amd {
+
+constexpr int kMaxSteps = 2048;  // block.cu:88, torsion.cu:97 (512 threads x 4 items)
+
+// Long chains: per-(chain, segment) state and backward scratch, in doubles.
+constexpr int kLongStateDoubles = 24;
+constexpr int kLongWorkDoubles = 12;
+// Default segment length: the largest plan capacity (2048 steps) unless the grid would then
+// hold fewer than ~4 workgroups per CU; halved down to 256 steps until it does.
+constexpr int64_t kLongMinSegment = 256;
+constexpr int64_t kLongTargetGroups = 1024;
+// Grid extents of the long-chain launches count work-items in 32 bits.
+constexpr int64_t kLongMaxGroups = int64_t{UINT32_MAX} / 256;
+
+inline int64_t long_segments(int64_t points, int64_t seg_steps) { return (points - 3 + seg_steps - 1) / seg_steps; }
+
+// ---------------------------------------------------------------------------- typed launchers
+// Each returns a cufk_status.  Pointers are device rows of B chains of N points; `anchor`
+// (optional) receives each chain's six anchor sums (F, tau) for anchor_grads_typed.
+
+// Forward, one chain per workgroup or packed (short chains, large batches).
+template <typename T>
+int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz,
+                          uint8_t* regular, int64_t B, int N, hipStream_t st);
+
+// Backward without a saved output: the forward scan is rerun per chain.
+template <typename T>
+int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
+                                    const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st,
+                                    double* anchor = nullptr);
+
+// Backward over the saved forward output and its regularity flags (float and double only).
+template <typename T>
+int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
+                                const T* xyz, const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N,
+                                hipStream_t st, double* anchor = nullptr);
+
+// Batch reduction of the anchor sums and the map to the anchor gradients.
+template <typename T>
+int anchor_grads_typed(const double* anchor, int64_t B, const T* fd, const T* n0, T* grad_p0, T* grad_fd, T* grad_n0,
+                       hipStream_t st);
+
+// Short chains packed several per wave (called by the two functions above).
+template <typename T>
+int packed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz,
+                     uint8_t* regular, int64_t B, int N, hipStream_t st);
+template <typename T, bool Saved>
+int packed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st,
+                     double* anchor = nullptr);
+
+// Fused coordinate loss.
+template <typename T>
+int loss_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target, T* xyz,
+                   uint8_t* regular, T* loss, int64_t B, int N, hipStream_t st);
+template <typename T>
+int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                   const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
+                   hipStream_t st);
+
+// Chains past the single-workgroup cap, in segments of S steps.
+template <typename T>
+int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, double* state,
+                   int64_t B, int N, int S, hipStream_t st);
+template <typename T>
+int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                   const double* state, const T* g, double* work, T* gL, T* gA, T* gD, int64_t B, int N, int S,
+                   hipStream_t st);
+
+// Torsion path.
+template <typename T>
+int torsion_fwd_typed(const T* raw, int64_t rs, const TorsionArgs& c, T* xyz, int64_t B, int N, hipStream_t st);
+template <typename T>
+int torsion_bwd_typed(const T* raw, int64_t rs, const T* xyz, const T* g, T* graw, int64_t gs, const TorsionArgs& c,
+                      int64_t B, int N, hipStream_t st);
+
+}  // namespace cufk_amd

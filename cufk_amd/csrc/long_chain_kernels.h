@@ -25,13 +25,12 @@
 #include <cstdint>
 
 #include "chain_ops.h"
+#include "launch.h"
 #include "reconstruct_kernels.h"
 #include "staging.h"
 
 namespace cufk_amd {
 
-constexpr int kLongStateDoubles = 24;
-constexpr int kLongWorkDoubles = 12;
 constexpr int kLongThreads = 256;  // per-point and per-chain passes
 
 struct SegmentOf {
@@ -200,9 +199,9 @@ __global__ __launch_bounds__(kLongThreads) void long_backward_sums_kernel(const 
 // world origin (W = M + x2 x F for a segment's own sums), the carry of segment j is
 // F = sum_{l>j} F_l and M = sum_{l>j} W_l - x2_j x F: an exclusive suffix sum over segments,
 // lane l holding segment 64c + l, chunks from the last.
-__global__ __launch_bounds__(kLongThreads) void long_backward_carry_kernel(const double* __restrict__ state,
-                                                                          double* __restrict__ work, int64_t batch,
-                                                                          int segments) {
+static __global__ __launch_bounds__(kLongThreads) void long_backward_carry_kernel(const double* __restrict__ state,
+                                                                                 double* __restrict__ work,
+                                                                                 int64_t batch, int segments) {
   const int lane = threadIdx.x & 63;
   const int64_t b = static_cast<int64_t>(blockIdx.x) * (kLongThreads / 64) + (threadIdx.x >> 6);
   if (b >= batch) return;  // uniform per wave
