@@ -89,54 +89,168 @@ __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
     if (fabsf(xf) > kWideReduceMax) sincos(x, &s, &c);
   }
 }
-// sin and cos of a float argument from a 16-entry table and short polynomials, for the hot
-// loop of the forward: k = rint(8x/pi), r = x - k pi/8 (two-part Cody-Waite) with |r| <= pi/16,
-//   sin r = r + r u (s1 + s2 u + s3 u^2),  cos r = 1 + u (c1 + c2 u + c3 u^2 + c4 u^3),  u = r^2
-// (Chebyshev fits: |error| < 4e-14 and < 2e-16), then
-//   sin x = T_s[k] cos r + T_c[k] sin r,  cos x = T_c[k] cos r - T_s[k] sin r
-// with (T_s, T_c)[j] = (sin, cos)(j pi/8) held in LDS (sin_cos_table_init).  No quadrant
-// selects; about 22 VALU issues against 30 for sin_cos_wide.  Same Checked convention.
-struct SinCosEntry {
+// sin and cos of a float argument from a 128-entry table and degree-1 polynomials, for the hot
+// loops of the forward kernels:
+//   t = x * 64/pi + 1.5 * 2^52 rounds k = rint(64 x / pi) into the low mantissa bits of t,
+//   r = x - k pi/64 (one-part reduction: |r| <= pi/128, absolute error <= |k| 2^-58, i.e.
+//       4.4e-16 for |x| <= 2 pi and 4.7e-12 at kWideReduceMax),
+//   sin r = r + r u (s1 + s2 u),  cos r = 1 + w,  w = u (c1 + c2 u),  u = r^2
+//   (near-minimax Chebyshev fits on [0, (pi/128)^2]: |error| < 1.4e-16 and < 3.8e-14),
+//   sin x = T_s[k] + T_s[k] w + T_c[k] sin r,  cos x = T_c[k] + T_c[k] w - T_s[k] sin r
+// with (T_s, T_c)[j] = (sin, cos)(j pi/64) held in LDS (sin_cos_table_init) and indexed by the
+// low 7 bits of t.  No quadrant selects or conversions to integer: 18 VALU issues.  Same
+// Checked convention as sin_cos_wide.
+struct __align__(16) SinCosEntry {
   double s, c;
 };
-constexpr int kSinCosTable = 16;
-__device__ __forceinline__ void sin_cos_table_init(SinCosEntry* table, int tid) {
+constexpr int kSinCosTable = 128;
+__device__ __forceinline__ void sin_cos_table_init(SinCosEntry* table, int tid, int threads) {
   constexpr double kTable[kSinCosTable][2] = {
-    {0.0, 1.0},
-    {0.3826834323650898, 0.9238795325112867},
-    {0.7071067811865476, 0.7071067811865476},
-    {0.9238795325112867, 0.3826834323650898},
-    {1.0, 0.0},
-    {0.9238795325112867, -0.3826834323650898},
-    {0.7071067811865476, -0.7071067811865476},
-    {0.3826834323650898, -0.9238795325112867},
-    {0.0, -1.0},
-    {-0.3826834323650898, -0.9238795325112867},
-    {-0.7071067811865476, -0.7071067811865476},
-    {-0.9238795325112867, -0.3826834323650898},
-    {-1.0, 0.0},
-    {-0.9238795325112867, 0.3826834323650898},
-    {-0.7071067811865476, 0.7071067811865476},
-    {-0.3826834323650898, 0.9238795325112867}};
-  if (tid < kSinCosTable) table[tid] = SinCosEntry{kTable[tid][0], kTable[tid][1]};
+  {0.0, 1.0},
+  {0.049067674327418015, 0.9987954562051724},
+  {0.0980171403295606, 0.9951847266721969},
+  {0.14673047445536175, 0.989176509964781},
+  {0.19509032201612828, 0.9807852804032304},
+  {0.2429801799032639, 0.970031253194544},
+  {0.2902846772544624, 0.9569403357322088},
+  {0.33688985339222005, 0.9415440651830208},
+  {0.3826834323650898, 0.9238795325112867},
+  {0.4275550934302821, 0.9039892931234433},
+  {0.47139673682599764, 0.881921264348355},
+  {0.5141027441932218, 0.8577286100002721},
+  {0.5555702330196022, 0.8314696123025452},
+  {0.5956993044924334, 0.8032075314806449},
+  {0.6343932841636455, 0.773010453362737},
+  {0.6715589548470184, 0.7409511253549591},
+  {0.7071067811865476, 0.7071067811865476},
+  {0.7409511253549591, 0.6715589548470184},
+  {0.773010453362737, 0.6343932841636455},
+  {0.8032075314806449, 0.5956993044924334},
+  {0.8314696123025452, 0.5555702330196022},
+  {0.8577286100002721, 0.5141027441932218},
+  {0.881921264348355, 0.47139673682599764},
+  {0.9039892931234433, 0.4275550934302821},
+  {0.9238795325112867, 0.3826834323650898},
+  {0.9415440651830208, 0.33688985339222005},
+  {0.9569403357322088, 0.2902846772544624},
+  {0.970031253194544, 0.2429801799032639},
+  {0.9807852804032304, 0.19509032201612828},
+  {0.989176509964781, 0.14673047445536175},
+  {0.9951847266721969, 0.0980171403295606},
+  {0.9987954562051724, 0.049067674327418015},
+  {1.0, 0.0},
+  {0.9987954562051724, -0.049067674327418015},
+  {0.9951847266721969, -0.0980171403295606},
+  {0.989176509964781, -0.14673047445536175},
+  {0.9807852804032304, -0.19509032201612828},
+  {0.970031253194544, -0.2429801799032639},
+  {0.9569403357322088, -0.2902846772544624},
+  {0.9415440651830208, -0.33688985339222005},
+  {0.9238795325112867, -0.3826834323650898},
+  {0.9039892931234433, -0.4275550934302821},
+  {0.881921264348355, -0.47139673682599764},
+  {0.8577286100002721, -0.5141027441932218},
+  {0.8314696123025452, -0.5555702330196022},
+  {0.8032075314806449, -0.5956993044924334},
+  {0.773010453362737, -0.6343932841636455},
+  {0.7409511253549591, -0.6715589548470184},
+  {0.7071067811865476, -0.7071067811865476},
+  {0.6715589548470184, -0.7409511253549591},
+  {0.6343932841636455, -0.773010453362737},
+  {0.5956993044924334, -0.8032075314806449},
+  {0.5555702330196022, -0.8314696123025452},
+  {0.5141027441932218, -0.8577286100002721},
+  {0.47139673682599764, -0.881921264348355},
+  {0.4275550934302821, -0.9039892931234433},
+  {0.3826834323650898, -0.9238795325112867},
+  {0.33688985339222005, -0.9415440651830208},
+  {0.2902846772544624, -0.9569403357322088},
+  {0.2429801799032639, -0.970031253194544},
+  {0.19509032201612828, -0.9807852804032304},
+  {0.14673047445536175, -0.989176509964781},
+  {0.0980171403295606, -0.9951847266721969},
+  {0.049067674327418015, -0.9987954562051724},
+  {0.0, -1.0},
+  {-0.049067674327418015, -0.9987954562051724},
+  {-0.0980171403295606, -0.9951847266721969},
+  {-0.14673047445536175, -0.989176509964781},
+  {-0.19509032201612828, -0.9807852804032304},
+  {-0.2429801799032639, -0.970031253194544},
+  {-0.2902846772544624, -0.9569403357322088},
+  {-0.33688985339222005, -0.9415440651830208},
+  {-0.3826834323650898, -0.9238795325112867},
+  {-0.4275550934302821, -0.9039892931234433},
+  {-0.47139673682599764, -0.881921264348355},
+  {-0.5141027441932218, -0.8577286100002721},
+  {-0.5555702330196022, -0.8314696123025452},
+  {-0.5956993044924334, -0.8032075314806449},
+  {-0.6343932841636455, -0.773010453362737},
+  {-0.6715589548470184, -0.7409511253549591},
+  {-0.7071067811865476, -0.7071067811865476},
+  {-0.7409511253549591, -0.6715589548470184},
+  {-0.773010453362737, -0.6343932841636455},
+  {-0.8032075314806449, -0.5956993044924334},
+  {-0.8314696123025452, -0.5555702330196022},
+  {-0.8577286100002721, -0.5141027441932218},
+  {-0.881921264348355, -0.47139673682599764},
+  {-0.9039892931234433, -0.4275550934302821},
+  {-0.9238795325112867, -0.3826834323650898},
+  {-0.9415440651830208, -0.33688985339222005},
+  {-0.9569403357322088, -0.2902846772544624},
+  {-0.970031253194544, -0.2429801799032639},
+  {-0.9807852804032304, -0.19509032201612828},
+  {-0.989176509964781, -0.14673047445536175},
+  {-0.9951847266721969, -0.0980171403295606},
+  {-0.9987954562051724, -0.049067674327418015},
+  {-1.0, 0.0},
+  {-0.9987954562051724, 0.049067674327418015},
+  {-0.9951847266721969, 0.0980171403295606},
+  {-0.989176509964781, 0.14673047445536175},
+  {-0.9807852804032304, 0.19509032201612828},
+  {-0.970031253194544, 0.2429801799032639},
+  {-0.9569403357322088, 0.2902846772544624},
+  {-0.9415440651830208, 0.33688985339222005},
+  {-0.9238795325112867, 0.3826834323650898},
+  {-0.9039892931234433, 0.4275550934302821},
+  {-0.881921264348355, 0.47139673682599764},
+  {-0.8577286100002721, 0.5141027441932218},
+  {-0.8314696123025452, 0.5555702330196022},
+  {-0.8032075314806449, 0.5956993044924334},
+  {-0.773010453362737, 0.6343932841636455},
+  {-0.7409511253549591, 0.6715589548470184},
+  {-0.7071067811865476, 0.7071067811865476},
+  {-0.6715589548470184, 0.7409511253549591},
+  {-0.6343932841636455, 0.773010453362737},
+  {-0.5956993044924334, 0.8032075314806449},
+  {-0.5555702330196022, 0.8314696123025452},
+  {-0.5141027441932218, 0.8577286100002721},
+  {-0.47139673682599764, 0.881921264348355},
+  {-0.4275550934302821, 0.9039892931234433},
+  {-0.3826834323650898, 0.9238795325112867},
+  {-0.33688985339222005, 0.9415440651830208},
+  {-0.2902846772544624, 0.9569403357322088},
+  {-0.2429801799032639, 0.970031253194544},
+  {-0.19509032201612828, 0.9807852804032304},
+  {-0.14673047445536175, 0.989176509964781},
+  {-0.0980171403295606, 0.9951847266721969},
+  {-0.049067674327418015, 0.9987954562051724}};
+  for (int j = tid; j < kSinCosTable; j += threads) table[j] = SinCosEntry{kTable[j][0], kTable[j][1]};
 }
 template <bool Checked = true>
 __device__ __forceinline__ void sin_cos_tab(float xf, const SinCosEntry* table, double& s, double& c) {
+  constexpr double kRound = 6755399441055744.0;  // 1.5 * 2^52: ulp 1 over [2^52, 2^53)
   const double x = xf;
-  const double k = __builtin_rint(x * 2.5464790894703255);
-  double r = fma(-k, 0.39269908169872414, x);
-  r = fma(-k, 1.5308084989341915e-17, r);
+  const double t = fma(x, 20.371832715762604, kRound);
+  const double k = t - kRound;
+  const double r = fma(-k, 0.04908738521234052, x);
   const double u = r * r;
-  double ps = lin_sk(u, -0.00019825339804578352, 0.008333331030517558);
-  ps = fma_sk(ps, u, -0.1666666666617345);
+  const double ps = lin_sk(u, 0.008333213811818094, -0.1666666666576668);
   const double sr = fma(r * u, ps, r);
-  double pc = lin_sk(u, 2.478034740778822e-05, -0.0013888883771620158);
-  pc = fma_sk(pc, u, 0.041666666662721126);
-  pc = fma_sk(pc, u, -0.4999999999999952);
-  const double cr = fma_sk(u, pc, 1.0);
-  const SinCosEntry t = table[static_cast<int>(k) & (kSinCosTable - 1)];
-  s = fma(t.s, cr, t.c * sr);
-  c = fma(t.c, cr, -(t.s * sr));
+  const double pc = lin_sk(u, 0.04166583001780997, -0.49999999993700117);
+  const double w = u * pc;
+  const SinCosEntry e = table[static_cast<uint32_t>(__builtin_bit_cast(uint64_t, t)) & (kSinCosTable - 1)];
+  s = fma(e.s, w, fma(e.c, sr, e.s));
+  c = fma(e.c, w, fma(-e.s, sr, e.c));
   if constexpr (Checked) {
     if (fabsf(xf) > kWideReduceMax) sincos(x, &s, &c);
   }
@@ -172,6 +286,14 @@ template <typename R> __device__ __forceinline__ void pair_unit(R rs, R rc, doub
   S = a * rinv;
   C = b * rinv;
 }
+
+// Minimum of two bond lengths for the regularity test.  Positive floats order as their bit
+// patterns do as integers (one v_min_i32 instead of a canonicalising fmin); a chain with a
+// non-positive or NaN length fails that test whatever this returns.
+__device__ __forceinline__ float min_positive(float a, float b) {
+  return __builtin_bit_cast(float, min(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b)));
+}
+__device__ __forceinline__ double min_positive(double a, double b) { return fmin(a, b); }
 
 __device__ __forceinline__ float sqrt_r(float x) { return sqrtf(x); }
 __device__ __forceinline__ double sqrt_r(double x) { return sqrt(x); }

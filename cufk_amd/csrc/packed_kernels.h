@@ -303,7 +303,7 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
 
   bool wide = stage_params<P>(rows, lengths + b0 * (points - 1), angles + b0 * (points - 2),
                               dihedrals + b0 * (points - 3), nc, points, tid);
-  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid);
+  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, 64 * W);
   wide = block_any<W>(wide, wide_vote, lane, wave);  // barrier: rows and table visible
 
   FirstFrame<R> ff;

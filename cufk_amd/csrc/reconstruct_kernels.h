@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <limits>
 #include <type_traits>
 
 #include "chain_ops.h"
@@ -119,6 +120,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   const int wave = tid >> 6;
   const int s0 = tid * K;
   const int count = steps - s0 < K ? steps - s0 : K;  // items of this lane (may be <= 0)
+  const int b0 = Lay::lane_step_base(tid);
 
   bool wide;  // some angle of the chain needs the library sin/cos
   {
@@ -126,7 +128,19 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
-  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid);
+  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, Lay::kLanes);
+  if constexpr (!Segmented) {
+    // The lane holding the last step pads the rest of its items with steps that pass the
+    // regularity tests (longest bond, right angle, no twist), so the serial scan below runs
+    // every item unguarded; they follow the chain's last point and feed nothing stored.
+    if (count > 0 && count < K) {
+      for (int i = count; i < K; ++i) {
+        stage[b0 + i] = std::numeric_limits<R>::max();
+        stage[Lay::kStepRow + b0 + i] = R(1.5707963267948966);
+        stage[2 * Lay::kStepRow + b0 + i] = R(0);
+      }
+    }
+  }
   // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
   if constexpr (Loss) load_run<3 * K>(target + 9 + 3 * s0, count > 0 ? 3 * count : 0, tr);
@@ -152,15 +166,19 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   // translation of the lane-local prefix after item i.  Items are read from LDS as the scan
   // reaches them, so only y stays in registers.  The library sin/cos is compiled into a
   // second instance of the loop that runs only for chains with out-of-range angles.
-  const int b0 = Lay::lane_step_base(tid);
+  // For a whole chain the hot instance runs every item of every lane unguarded (the last
+  // lane's tail is padded above; lanes past the chain scan garbage that reaches no stored
+  // point, and reset their flags afterwards); waves past the chain skip the loop.  Segments
+  // keep the guard (their last lane's total transform is stored), and so does the library
+  // instance, whose unguarded form needs more registers than the hot one.
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
-  auto serial = [&]<bool Checked>() {
+  auto serial = [&]<bool Checked, bool Guard>() {
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      if (i < count) {
+      if (!Guard || i < count) {
         const R l = stage[b0 + i];
         double s, c, S, C;
         if constexpr (sizeof(R) == 4) {
@@ -172,17 +190,33 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         }
         step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
         ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
-        lmin = fmin(lmin, l);
+        lmin = min_positive(lmin, l);
       }
       y[i][0] = static_cast<R>(q.v[0]);
       y[i][1] = static_cast<R>(q.v[1]);
       y[i][2] = static_cast<R>(q.v[2]);
+      // One scheduling region per item: hoisting the independent sin/cos of later items
+      // would hold them all in registers at once.
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  if (wide)
-    serial.template operator()<true>();
-  else
-    serial.template operator()<false>();
+  if constexpr (Segmented) {
+    if (wide)
+      serial.template operator()<true, true>();
+    else
+      serial.template operator()<false, true>();
+  } else {
+    if (wave * 64 * K < steps) {  // uniform per wave
+      if (wide)
+        serial.template operator()<true, true>();  // cold: guarded, which holds fewer registers
+      else
+        serial.template operator()<false, false>();
+    }
+    if (count <= 0) {
+      ok = true;
+      lmin = R(1.0e30);
+    }
+  }
 
   // lane_carry's barrier also publishes base[] and retires every read of the staged step
   // rows, which the point row below overwrites.
