@@ -12,13 +12,17 @@ The timed steps rotate over ``--sets`` independent input batches (3 by default, 
 at config 2), so no step finds its inputs in the 256 MB last-level cache left behind by the
 previous one.  HIP events recorded inside the timed region on the stream the kernels run on
 (the current torch stream, which the extension launches on) bracket the K timed steps; a second
-pass of K steps with an event between forward and backward splits the step.  ``roofline`` is
-for the backward (the larger one): its algorithmic bytes per launch are 4*B*(9N-12) (read
-lengths, angles, dihedrals and grad_xyz, write the three gradients), divided by the average
-duration of the backward entry point the autograd path calls, timed through the C ABI over
-back-to-back launches rotating over the same input sets, against MI355X's 8 TB/s HBM peak.  ``traffic`` is the
-HBM bytes per launch the rocprofv3 FETCH_SIZE and WRITE_SIZE counters read for the same kernel,
-copied from the committed summaries under profiles/ (MEASURED_TRAFFIC below).
+pass of K steps puts events around each step's forward call and around its backward node
+(autograd pre- and post-hooks), which splits the step.  ``roofline`` is for the backward: its
+algorithmic bytes per launch are 4*B*(9N-12) (read lengths, angles, dihedrals and grad_xyz,
+write the three gradients), divided by the backward node's average duration over that second
+pass (the kernel as the timed steps run it, which is what rocprofv3's kernel trace of the same
+command averages), against MI355X's 8 TB/s HBM peak.  ``traffic`` is the HBM bytes per launch
+the rocprofv3 FETCH_SIZE and WRITE_SIZE counters read for the same kernel, copied from the
+committed summaries under profiles/ (MEASURED_TRAFFIC below).  ``abi_*_us`` time each C-ABI
+entry point alone over back-to-back launches rotating over the input sets (an event pair per
+launch); a backward launched after another backward, not after its forward, no longer finds the
+forward's output in the last-level cache, so those run slower than in the step.
 
 The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host on a bounded
 sample of chains of the same shape (chunks of about 128 x 2049 points until about 15 s of work),
@@ -113,19 +117,19 @@ def synthetic(B, N, seed, torch, device, dtype):
 
 
 def event_time_ms(torch, fn, reps):
-    """Average time of fn(i) over reps back-to-back calls (i = 0..reps-1), HIP events on the
-    current stream."""
+    """Average duration of fn(i) over reps back-to-back calls (i = 0..reps-1): a pair of HIP
+    events on the current stream brackets each call, so the average is the launch's own
+    duration (what rocprofv3's kernel trace reports), without the gaps between launches."""
     stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     fn(0)
     torch.cuda.synchronize()
-    start.record(stream)
     for i in range(reps):
+        marks[i][0].record(stream)
         fn(i)
-    end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) / reps
+        marks[i][1].record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in marks) / reps
 
 
 def cpu_baseline(kind, B, N, sample, seconds):
@@ -219,7 +223,7 @@ def main():
             def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
                 xyz = cufk_amd.reconstruct_long(L, A, D, p0, fd, n0)
                 if mark is not None:
-                    mark.record()
+                    mark(xyz)
                 return torch.autograd.grad(xyz, (L, A, D), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -258,7 +262,7 @@ def main():
             def step(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, mark=None):
                 loss = cufk_amd.reconstruct_loss(L, A, D, target, p0, fd, n0)
                 if mark is not None:
-                    mark.record()
+                    mark(loss)
                 return torch.autograd.grad(loss.sum(), (L, A, D))
 
             def plain(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
@@ -296,7 +300,7 @@ def main():
             def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
                 xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
                 if mark is not None:
-                    mark.record()
+                    mark(xyz)
                 return torch.autograd.grad(xyz, (L, A, D), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -339,7 +343,7 @@ def main():
             def step(raw=raw, g=g, mark=None):
                 xyz = f(raw)
                 if mark is not None:
-                    mark.record()
+                    mark(xyz)
                 return torch.autograd.grad(xyz, (raw,), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -374,17 +378,27 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
 
-    # The same K steps again with an event between each step's forward and backward (the
-    # extra event packets cost a few microseconds per step, so this pass is reported apart).
-    marks = [(ev(), ev()) for _ in range(args.steps + 1)]
+    # The same K steps again with events around each step's forward call and around its
+    # backward node (autograd pre- and post-hooks on the output's grad_fn, run on the same
+    # stream right before and after the node launches its kernel).  The extra event packets
+    # cost a little per step, so this pass is reported apart from ms_per_step.
+    marks = [(ev(), ev(), ev(), ev()) for _ in range(args.steps)]
+
+    def marker(m):
+        def mark(out):
+            m[1].record(stream)
+            out.grad_fn.register_prehook(lambda grad_out: m[2].record(stream))
+            out.grad_fn.register_hook(lambda grad_in, grad_out: m[3].record(stream))
+
+        return mark
+
     torch.cuda.synchronize()
     for i in range(args.steps):
         marks[i][0].record(stream)
-        steps[i % nsets](mark=marks[i][1])
-    marks[args.steps][0].record(stream)
+        steps[i % nsets](mark=marker(marks[i]))
     torch.cuda.synchronize()
-    seg_fwd = sum(marks[i][0].elapsed_time(marks[i][1]) for i in range(args.steps)) / args.steps
-    seg_bwd = sum(marks[i][1].elapsed_time(marks[i + 1][0]) for i in range(args.steps)) / args.steps
+    seg_fwd = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
+    seg_bwd = sum(m[2].elapsed_time(m[3]) for m in marks) / args.steps
 
     # Kernel-level timing straight through the C ABI, rotating over the same sets.
     st = ctypes.c_void_p(stream.cuda_stream)
@@ -406,8 +420,8 @@ def main():
         unfused_us = u0.elapsed_time(u1) / args.steps * 1e3
 
     atoms = B * N
-    bw_bwd = bwd_bytes / (t_bwd * 1e-3) / 1e9
-    bw_fwd = fwd_bytes / (t_fwd * 1e-3) / 1e9
+    bw_bwd = bwd_bytes / (seg_bwd * 1e-3) / 1e9  # the backward kernel as the timed steps run it
+    bw_fwd = fwd_bytes / (seg_fwd * 1e-3) / 1e9
     traffic = MEASURED_TRAFFIC.get((args.config, f"{kind}_backward"))
     result = {
         "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
@@ -433,15 +447,15 @@ def main():
             "frac": bw_bwd / HBM_PEAK_GBS,
             "traffic": traffic,
             "algorithmic_bytes": bwd_bytes,
-            "avg_launch_us": t_bwd * 1e3,
+            "avg_launch_us": seg_bwd * 1e3,
         },
         "kernels": {
             "step_forward_us": seg_fwd * 1e3,
             "step_backward_us": seg_bwd * 1e3,
+            "step_forward_GBs": bw_fwd,
+            "step_backward_GBs": bw_bwd,
             "abi_forward_us": t_fwd * 1e3,
             "abi_backward_us": t_bwd * 1e3,
-            "abi_forward_GBs": bw_fwd,
-            "abi_backward_GBs": bw_bwd,
             "step_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "regular_chain_fraction": regular_frac,
             "unfused_step_us": unfused_us,

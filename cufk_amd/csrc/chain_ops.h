@@ -41,6 +41,13 @@ __device__ __forceinline__ double fma_sk(double a, double b, double c) {
   asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(c));
   return d;
 }
+// a * k - 0.5 for a constant k kept in a scalar register pair (-0.5 is an inline constant,
+// which does not count against VOP3's one scalar operand): one v_fma_f64.
+__device__ __forceinline__ double fma_sk_minus_half(double a, double k) {
+  double d;
+  asm("v_fma_f64 %0, %1, %2, -0.5" : "=v"(d) : "v"(a), "s"(k));
+  return d;
+}
 // c0 * u + c1 for constants c0, c1: v_mul_f64 and v_add_f64, each with a scalar operand.
 __device__ __forceinline__ double lin_sk(double u, double c0, double c1) {
   double t, d;
@@ -94,11 +101,12 @@ __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
 //   t = x * 64/pi + 1.5 * 2^52 rounds k = rint(64 x / pi) into the low mantissa bits of t,
 //   r = x - k pi/64 (one-part reduction: |r| <= pi/128, absolute error <= |k| 2^-58, i.e.
 //       4.4e-16 for |x| <= 2 pi and 4.7e-12 at kWideReduceMax),
-//   sin r = r + r u (s1 + s2 u),  cos r = 1 + w,  w = u (c1 + c2 u),  u = r^2
-//   (near-minimax Chebyshev fits on [0, (pi/128)^2]: |error| < 1.4e-16 and < 3.8e-14),
+//   sin r = r + r u (s1 + s2 u),  cos r = 1 + w,  w = u (c2 u - 1/2),  u = r^2
+//   (near-minimax fits on [0, (pi/128)^2], the cos one with its u term held at -1/2, an
+//   inline constant: |error| < 1.4e-16 and < 3.3e-14),
 //   sin x = T_s[k] + T_s[k] w + T_c[k] sin r,  cos x = T_c[k] + T_c[k] w - T_s[k] sin r
 // with (T_s, T_c)[j] = (sin, cos)(j pi/64) held in LDS (sin_cos_table_init) and indexed by the
-// low 7 bits of t.  No quadrant selects or conversions to integer: 18 VALU issues.  Same
+// low 7 bits of t.  No quadrant selects or conversions to integer: 17 VALU issues.  Same
 // Checked convention as sin_cos_wide.
 struct __align__(16) SinCosEntry {
   double s, c;
@@ -246,7 +254,7 @@ __device__ __forceinline__ void sin_cos_tab(float xf, const SinCosEntry* table, 
   const double u = r * r;
   const double ps = lin_sk(u, 0.008333213811818094, -0.1666666666576668);
   const double sr = fma(r * u, ps, r);
-  const double pc = lin_sk(u, 0.04166583001780997, -0.49999999993700117);
+  const double pc = fma_sk_minus_half(u, 0.04166591860459361);
   const double w = u * pc;
   const SinCosEntry e = table[static_cast<uint32_t>(__builtin_bit_cast(uint64_t, t)) & (kSinCosTable - 1)];
   s = fma(e.s, w, fma(e.c, sr, e.s));
@@ -371,16 +379,39 @@ template <typename R>
 __device__ __forceinline__ void step_forward(R (&m)[9], R (&v)[3], R l, R s, R c, R S, R C) {
 #pragma unroll
   for (int r = 0; r < 3; ++r) {
+    // Explicit fmas: the compiler has no contraction to choose, so every kernel that runs a
+    // step (guarded or not, after step_first or not) rounds it identically.
     const R q0 = m[3 * r], q1 = m[3 * r + 1], q2 = m[3 * r + 2];
-    const R a1 = C * q1 + S * q2;
-    const R a2 = C * q2 - S * q1;
-    const R n0 = s * a1 - c * q0;
-    const R n1 = -(s * q0) - c * a1;
+    const R a1 = fma(C, q1, S * q2);
+    const R a2 = fma(C, q2, -(S * q1));
+    const R n0 = fma(s, a1, -(c * q0));
+    const R n1 = fma(-s, q0, -(c * a1));
     m[3 * r] = n0;
     m[3 * r + 1] = n1;
     m[3 * r + 2] = a2;
-    v[r] = v[r] + l * n0;
+    v[r] = fma(l, n0, v[r]);
   }
+}
+
+// step_forward from the identity: R = Rx(phi) * Rz(pi - theta), translation l * R[:,0]
+// (the reference local transform, affine.cuh:36-45), without composing onto an identity the
+// compiler cannot fold away.  Every value rounds as step_forward's would from the identity, and
+// the next step consumes them through explicit fmas only, so kernels that run the loop guarded
+// (one basic block per step) or unguarded produce the same bits.
+template <typename R>
+__device__ __forceinline__ void step_first(R (&m)[9], R (&v)[3], R l, R s, R c, R S, R C) {
+  m[0] = -c;
+  m[1] = -s;
+  m[2] = R(0);
+  m[3] = s * C;
+  m[4] = -(c * C);
+  m[5] = -S;
+  m[6] = s * S;
+  m[7] = -(c * S);
+  m[8] = C;
+  v[0] = l * m[0];
+  v[1] = l * m[3];
+  v[2] = l * m[6];
 }
 
 // Inverse of the rotation part of step_forward: R <- R * Rz(pi - theta)^T * Rx(phi)^T.

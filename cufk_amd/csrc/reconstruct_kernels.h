@@ -188,7 +188,10 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
           sin_cos_wide<Checked>(stage[Lay::kStepRow + b0 + i], s, c);
           sin_cos_wide<Checked>(stage[2 * Lay::kStepRow + b0 + i], S, C);
         }
-        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        if (i == 0)
+          step_first(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        else
+          step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
         ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
         lmin = min_positive(lmin, l);
       }
