@@ -79,6 +79,84 @@ __device__ __forceinline__ void store_anchor_sums(double* __restrict__ out, V3<R
   out[5] = tau.z;
 }
 
+// ============================================================================ lane scan
+
+// Lane-serial scan of one lane's K items in double: q is the lane-local prefix transform and
+// y[i] its translation after item i, rounded to R.  Item i reads its (length, angle,
+// dihedral) from Ls[i], As[i], Ds[i] (the lane's run of three step-layout LDS rows).  With
+// Guard only items < count run; without it every item runs, and the caller has padded the
+// lane's tail (pad_lane_tail) or ignores the lane.  ok and lmin accumulate the regularity
+// tests (Fast::kSinMin).  With Table, float angles take sin/cos from the LDS table.  Checked
+// selects the sin/cos form that handles angles beyond kWideReduceMax.  With Sched every item
+// is a scheduling region of its own, which keeps the independent sin/cos of later items from
+// being hoisted (and held in registers) where the compiler would otherwise do so.
+template <typename T, int K, bool Checked, bool Guard, bool Table, bool Sched, typename Fast = FastPath<T>>
+__device__ __forceinline__ void lane_scan(const compute_t<T>* Ls, const compute_t<T>* As, const compute_t<T>* Ds,
+                                          int count, const SinCosEntry* table, Rigid<double>& q,
+                                          compute_t<T> (&y)[K][3], bool& ok, compute_t<T>& lmin) {
+  using R = compute_t<T>;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (!Guard || i < count) {
+      const R l = Ls[i];
+      double s, c, S, C;
+      if constexpr (Table && sizeof(R) == 4) {
+        sin_cos_tab<Checked>(As[i], table, s, c);
+        sin_cos_tab<Checked>(Ds[i], table, S, C);
+      } else {
+        sin_cos_wide<Checked>(As[i], s, c);
+        sin_cos_wide<Checked>(Ds[i], S, C);
+      }
+      if (i == 0)
+        step_first(q.m, q.v, static_cast<double>(l), s, c, S, C);
+      else
+        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+      ok = ok && l > R(0) && s >= Fast::kSinMin;
+      lmin = min_positive(lmin, l);
+    }
+    y[i][0] = static_cast<R>(q.v[0]);
+    y[i][1] = static_cast<R>(q.v[1]);
+    y[i][2] = static_cast<R>(q.v[2]);
+    if constexpr (Sched) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The lane holding the chain's last step pads the rest of its items in the three step rows
+// with steps that pass the regularity tests (longest bond, right angle, no twist), so that
+// lane_scan can run every item unguarded; they follow the chain's last point and feed
+// nothing that is stored.  Call before the barrier that publishes the rows.
+template <int K, typename R>
+__device__ __forceinline__ void pad_lane_tail(R* Ls, R* As, R* Ds, int count) {
+  if (count > 0 && count < K) {
+    for (int i = count; i < K; ++i) {
+      Ls[i] = std::numeric_limits<R>::max();
+      As[i] = R(1.5707963267948966);
+      Ds[i] = R(0);
+    }
+  }
+}
+
+// lane_scan over a whole chain: the hot instance unguarded (waves past the chain skip it;
+// lanes past it scan garbage that reaches no stored point and reset their flags), the
+// library-sin/cos instance guarded and one region per item (unguarded or unscheduled it needs
+// more registers than the hot one).
+template <typename T, int K, bool Table, bool Sched, typename Fast = FastPath<T>>
+__device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const compute_t<T>* As,
+                                                const compute_t<T>* Ds, int count, bool wave_has_steps, bool wide,
+                                                const SinCosEntry* table, Rigid<double>& q, compute_t<T> (&y)[K][3],
+                                                bool& ok, compute_t<T>& lmin) {
+  if (wave_has_steps) {  // uniform per wave
+    if (wide)
+      lane_scan<T, K, true, true, Table, true, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
+    else
+      lane_scan<T, K, false, false, Table, Sched, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
+  }
+  if (count <= 0) {
+    ok = true;
+    lmin = compute_t<T>(1.0e30);
+  }
+}
+
 // ============================================================================ forward
 
 // x0 = p0, x1, x2 from the first frame (block.cu:113-155), x_{k+3} = p2 + F P_k.v, for one
@@ -129,18 +207,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
   if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, Lay::kLanes);
-  if constexpr (!Segmented) {
-    // The lane holding the last step pads the rest of its items with steps that pass the
-    // regularity tests (longest bond, right angle, no twist), so the serial scan below runs
-    // every item unguarded; they follow the chain's last point and feed nothing stored.
-    if (count > 0 && count < K) {
-      for (int i = count; i < K; ++i) {
-        stage[b0 + i] = std::numeric_limits<R>::max();
-        stage[Lay::kStepRow + b0 + i] = R(1.5707963267948966);
-        stage[2 * Lay::kStepRow + b0 + i] = R(0);
-      }
-    }
-  }
+  if constexpr (!Segmented) pad_lane_tail<K>(stage + b0, stage + Lay::kStepRow + b0, stage + 2 * Lay::kStepRow + b0, count);
   // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
   if constexpr (Loss) load_run<3 * K>(target + 9 + 3 * s0, count > 0 ? 3 * count : 0, tr);
@@ -164,60 +231,25 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
 
   // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
   // translation of the lane-local prefix after item i.  Items are read from LDS as the scan
-  // reaches them, so only y stays in registers.  The library sin/cos is compiled into a
-  // second instance of the loop that runs only for chains with out-of-range angles.
-  // For a whole chain the hot instance runs every item of every lane unguarded (the last
-  // lane's tail is padded above; lanes past the chain scan garbage that reaches no stored
-  // point, and reset their flags afterwards); waves past the chain skip the loop.  Segments
-  // keep the guard (their last lane's total transform is stored), and so does the library
-  // instance, whose unguarded form needs more registers than the hot one.
+  // reaches them, so only y stays in registers.  Segments run it guarded: their last lane's
+  // total transform is stored.  Measured at C2 (5 waves per SIMD), the table beats
+  // sin_cos_wide (56.5 against 58.2 us).
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
-  auto serial = [&]<bool Checked, bool Guard>() {
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if (!Guard || i < count) {
-        const R l = stage[b0 + i];
-        double s, c, S, C;
-        if constexpr (sizeof(R) == 4) {
-          sin_cos_tab<Checked>(stage[Lay::kStepRow + b0 + i], sc_table, s, c);
-          sin_cos_tab<Checked>(stage[2 * Lay::kStepRow + b0 + i], sc_table, S, C);
-        } else {
-          sin_cos_wide<Checked>(stage[Lay::kStepRow + b0 + i], s, c);
-          sin_cos_wide<Checked>(stage[2 * Lay::kStepRow + b0 + i], S, C);
-        }
-        if (i == 0)
-          step_first(q.m, q.v, static_cast<double>(l), s, c, S, C);
-        else
-          step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
-        ok = ok && l > R(0) && s >= FastPath<T>::kSinMin;
-        lmin = min_positive(lmin, l);
-      }
-      y[i][0] = static_cast<R>(q.v[0]);
-      y[i][1] = static_cast<R>(q.v[1]);
-      y[i][2] = static_cast<R>(q.v[2]);
-      // One scheduling region per item: hoisting the independent sin/cos of later items
-      // would hold them all in registers at once.
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  if constexpr (Segmented) {
-    if (wide)
-      serial.template operator()<true, true>();
-    else
-      serial.template operator()<false, true>();
-  } else {
-    if (wave * 64 * K < steps) {  // uniform per wave
+  {
+    const R* const Ls = stage + b0;
+    const R* const As = stage + Lay::kStepRow + b0;
+    const R* const Ds = stage + 2 * Lay::kStepRow + b0;
+    constexpr bool kTable = sizeof(R) == 4;
+    if constexpr (Segmented) {
       if (wide)
-        serial.template operator()<true, true>();  // cold: guarded, which holds fewer registers
+        lane_scan<T, K, true, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
       else
-        serial.template operator()<false, false>();
-    }
-    if (count <= 0) {
-      ok = true;
-      lmin = R(1.0e30);
+        lane_scan<T, K, false, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
+    } else {
+      lane_scan_chain<T, K, kTable, true>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok, lmin);
     }
   }
 
@@ -677,6 +709,9 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
     const T* const gsrc[1] = {Gr};
     load_point_rows<Lay, 1>(gdst, gsrc, points, tid);
   }
+  // sin/cos without the LDS table: measured at C4 (bf16, 2 waves x 8 steps, 10 waves per CU)
+  // the table's bank conflicts cost more than its arithmetic saves (237 against 210 us).
+  pad_lane_tail<K>(pstage + b0, pstage + Lay::kStepRow + b0, pstage + 2 * Lay::kStepRow + b0, count);
   const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
   wide = block_any<W>(wide, wide_vote, lane, wave);
 
@@ -684,27 +719,8 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
-  auto serial = [&]<bool Checked>() {
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if (i < count) {
-        const R l = pstage[b0 + i];
-        double s, c, S, C;
-        sin_cos_wide<Checked>(pstage[Lay::kStepRow + b0 + i], s, c);
-        sin_cos_wide<Checked>(pstage[2 * Lay::kStepRow + b0 + i], S, C);
-        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
-        ok = ok && l > R(0) && s >= Fast::kSinMin;
-        lmin = fmin(lmin, l);
-      }
-      y[i][0] = static_cast<R>(q.v[0]);
-      y[i][1] = static_cast<R>(q.v[1]);
-      y[i][2] = static_cast<R>(q.v[2]);
-    }
-  };
-  if (wide)
-    serial.template operator()<true>();
-  else
-    serial.template operator()<false>();
+  lane_scan_chain<T, K, false, true, Fast>(pstage + b0, pstage + Lay::kStepRow + b0, pstage + 2 * Lay::kStepRow + b0,
+                                           count, wave * 64 * K < steps, wide, nullptr, q, y, ok, lmin);
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
 
   // World frame at the lane start, origin at x2.
