@@ -211,22 +211,6 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
   if constexpr (Loss) load_run<3 * K>(target + 9 + 3 * s0, count > 0 ? 3 * count : 0, tr);
-  FirstFrame<R> ff;
-  if (wave == 0) {
-    if (!Segmented || head) {
-      ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-      if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < 9; ++i) base[i] = ff.frame[i];
-        base[9] = ff.p2.x;
-        base[10] = ff.p2.y;
-        base[11] = ff.p2.z;
-      }
-    } else if (lane == 0) {
-#pragma unroll
-      for (int i = 0; i < 12; ++i) base[i] = (i == 0 || i == 4 || i == 8) ? R(1) : R(0);
-    }
-  }
   wide = block_any<W>(wide, wide_vote, lane, wave);
 
   // Lane-local serial scan in double (rounding only at the lane boundary); y[i] is the
@@ -250,6 +234,25 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         lane_scan<T, K, false, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
       lane_scan_chain<T, K, kTable, true>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok, lmin);
+    }
+  }
+
+  // The first frame (block.cu:113-148) after the lane scan: no other wave waits on it before
+  // lane_carry's barrier, which publishes base[].
+  FirstFrame<R> ff;
+  if (wave == 0) {
+    if (!Segmented || head) {
+      ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < 9; ++i) base[i] = ff.frame[i];
+        base[9] = ff.p2.x;
+        base[10] = ff.p2.y;
+        base[11] = ff.p2.z;
+      }
+    } else if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 12; ++i) base[i] = (i == 0 || i == 4 || i == 8) ? R(1) : R(0);
     }
   }
 
