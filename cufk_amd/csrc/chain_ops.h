@@ -515,6 +515,83 @@ template <typename R> __device__ __forceinline__ Rigid<R> wave_prefix(Rigid<R> x
   return x;
 }
 
+// One level of wave_prefix for float rigids, as one block of DPP-fused VALU operations: every
+// output starts as the lane's own entry, and v_mul/v_fmac with a DPP source (the earlier lane's
+// row) overwrite it on lanes whose source is in range (CTRL's row_shr / row_bcast pattern and
+// row mask); lanes without a source keep their own transform, the identity composition.  51
+// VALU issues against about 62 for compose() over dpp_rigid(), which first copies the 12
+// entries with identity defaults.  The s_nop at each end supplies the wait states a DPP read
+// needs after a VALU write of its source: the compiler does not count them across inline asm.
+#define CUFK_RIGID_DPP_LEVEL(CTRL, x, o) \
+  asm("s_nop 1\n" \
+      "v_mov_b32 %[o0], %[x0]\n" \
+      "v_mul_f32_dpp %[o0], %[x0], %[x0] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o0], %[x1], %[x3] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o0], %[x2], %[x6] " CTRL "\n" \
+      "v_mov_b32 %[o1], %[x1]\n" \
+      "v_mul_f32_dpp %[o1], %[x0], %[x1] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o1], %[x1], %[x4] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o1], %[x2], %[x7] " CTRL "\n" \
+      "v_mov_b32 %[o2], %[x2]\n" \
+      "v_mul_f32_dpp %[o2], %[x0], %[x2] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o2], %[x1], %[x5] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o2], %[x2], %[x8] " CTRL "\n" \
+      "v_mov_b32 %[o3], %[x3]\n" \
+      "v_mul_f32_dpp %[o3], %[x3], %[x0] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o3], %[x4], %[x3] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o3], %[x5], %[x6] " CTRL "\n" \
+      "v_mov_b32 %[o4], %[x4]\n" \
+      "v_mul_f32_dpp %[o4], %[x3], %[x1] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o4], %[x4], %[x4] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o4], %[x5], %[x7] " CTRL "\n" \
+      "v_mov_b32 %[o5], %[x5]\n" \
+      "v_mul_f32_dpp %[o5], %[x3], %[x2] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o5], %[x4], %[x5] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o5], %[x5], %[x8] " CTRL "\n" \
+      "v_mov_b32 %[o6], %[x6]\n" \
+      "v_mul_f32_dpp %[o6], %[x6], %[x0] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o6], %[x7], %[x3] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o6], %[x8], %[x6] " CTRL "\n" \
+      "v_mov_b32 %[o7], %[x7]\n" \
+      "v_mul_f32_dpp %[o7], %[x6], %[x1] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o7], %[x7], %[x4] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o7], %[x8], %[x7] " CTRL "\n" \
+      "v_mov_b32 %[o8], %[x8]\n" \
+      "v_mul_f32_dpp %[o8], %[x6], %[x2] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o8], %[x7], %[x5] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o8], %[x8], %[x8] " CTRL "\n" \
+      "v_mov_b32 %[o9], %[x9]\n" \
+      "v_mov_b32_dpp %[o9], %[x9] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o9], %[x0], %[x9] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o9], %[x1], %[x10] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o9], %[x2], %[x11] " CTRL "\n" \
+      "v_mov_b32 %[o10], %[x10]\n" \
+      "v_mov_b32_dpp %[o10], %[x10] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o10], %[x3], %[x9] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o10], %[x4], %[x10] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o10], %[x5], %[x11] " CTRL "\n" \
+      "v_mov_b32 %[o11], %[x11]\n" \
+      "v_mov_b32_dpp %[o11], %[x11] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o11], %[x6], %[x9] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o11], %[x7], %[x10] " CTRL "\n" \
+      "v_fmac_f32_dpp %[o11], %[x8], %[x11] " CTRL "\n" \
+      "s_nop 1" \
+      : [o0] "=&v"(o.m[0]), [o1] "=&v"(o.m[1]), [o2] "=&v"(o.m[2]), [o3] "=&v"(o.m[3]), [o4] "=&v"(o.m[4]), [o5] "=&v"(o.m[5]), [o6] "=&v"(o.m[6]), [o7] "=&v"(o.m[7]), [o8] "=&v"(o.m[8]), [o9] "=&v"(o.v[0]), [o10] "=&v"(o.v[1]), [o11] "=&v"(o.v[2]) \
+      : [x0] "v"(x.m[0]), [x1] "v"(x.m[1]), [x2] "v"(x.m[2]), [x3] "v"(x.m[3]), [x4] "v"(x.m[4]), [x5] "v"(x.m[5]), [x6] "v"(x.m[6]), [x7] "v"(x.m[7]), [x8] "v"(x.m[8]), [x9] "v"(x.v[0]), [x10] "v"(x.v[1]), [x11] "v"(x.v[2]))
+
+// wave_prefix for float rigids (the cross-lane scan of every float and half-type chain).
+__device__ __forceinline__ Rigid<float> wave_prefix(Rigid<float> x) {
+  Rigid<float> o;
+  CUFK_RIGID_DPP_LEVEL("row_shr:1 row_mask:0xf bank_mask:0xf", x, o);
+  CUFK_RIGID_DPP_LEVEL("row_shr:2 row_mask:0xf bank_mask:0xf", o, x);
+  CUFK_RIGID_DPP_LEVEL("row_shr:4 row_mask:0xf bank_mask:0xf", x, o);
+  CUFK_RIGID_DPP_LEVEL("row_shr:8 row_mask:0xf bank_mask:0xf", o, x);
+  CUFK_RIGID_DPP_LEVEL("row_bcast:15 row_mask:0xa bank_mask:0xf", x, o);
+  CUFK_RIGID_DPP_LEVEL("row_bcast:31 row_mask:0xc bank_mask:0xf", o, x);
+  return x;
+}
+#undef CUFK_RIGID_DPP_LEVEL
+
 // OR of a predicate over the workgroup: one vote per wave into flags[], then a barrier.
 // Uses W words of LDS (the compiler's __syncthreads_or reserves more).
 template <int W> __device__ __forceinline__ bool block_any(bool v, int (&flags)[W], int lane, int wave) {
