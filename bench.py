@@ -69,7 +69,7 @@ ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 # counter reads for a plain copy of known size; see profiles/reconstruct_c2_hbm_traffic.md.
 # Keyed by (config, kernel); a missing entry reports traffic as null.
 MEASURED_TRAFFIC = {
-    ("c2", "reconstruct_backward"): 303442035,  # 202614089 read (xyz, grad_xyz) + 100827947 written
+    ("c2", "reconstruct_backward"): 303494325,  # 202665849 read (xyz, grad_xyz) + 100828476 written
 }
 
 
