@@ -132,6 +132,32 @@ def event_time_ms(torch, fn, reps):
     return sum(a.elapsed_time(b) for a, b in marks) / reps
 
 
+def coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device, chains=64):
+    """Coordinate error of `dtype` against the float64 path on the same (rounded) inputs, over
+    `chains` chains drawn like the timed inputs (outside the timed region): RMS over chains and
+    coordinates, and max-abs, at chain positions 0, N/10, ..., N-1, plus over the whole chain.
+    The float64 path is the library's own (within 1e-12 of the CPU oracle in the GPU tests)."""
+    n = min(B, chains)
+    L, A, D, _, p0, fd, n0 = synthetic(n, N, 2, torch, device, dtype)
+    with torch.no_grad():
+        x = cufk_amd.reconstruct(L, A, D, p0, fd, n0).double()
+        r = cufk_amd.reconstruct(*(t.double() for t in (L, A, D, p0, fd, n0)))
+    d = x - r
+    rms_pos = d.pow(2).sum(-1).mean(0).sqrt()  # (N,)
+    max_pos = d.abs().amax(dim=(0, 2))
+    marks = sorted({round(i * (N - 1) / 10) for i in range(11)})
+    return {
+        "reference": "float64 reconstruct on the same rounded inputs",
+        "chains": n,
+        "unit": "input length unit (nm)",
+        "positions": marks,
+        "rms": [float(rms_pos[i]) for i in marks],
+        "max_abs": [float(max_pos[i]) for i in marks],
+        "rms_all": float(d.pow(2).sum(-1).mean().sqrt()),
+        "max_abs_all": float(d.abs().max()),
+    }
+
+
 def cpu_baseline(kind, B, N, sample, seconds):
     """Float64 oracle fwd + bwd on a bounded sample of chains, scaled to atoms/s.
 
@@ -419,6 +445,10 @@ def main():
         torch.cuda.synchronize()
         unfused_us = u0.elapsed_time(u1) / args.steps * 1e3
 
+    precision = None
+    if kind == "reconstruct":
+        precision = coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device)
+
     atoms = B * N
     bw_bwd = bwd_bytes / (seg_bwd * 1e-3) / 1e9  # the backward kernel as the timed steps run it
     bw_fwd = fwd_bytes / (seg_fwd * 1e-3) / 1e9
@@ -461,6 +491,8 @@ def main():
             "unfused_step_us": unfused_us,
         },
     }
+    if precision is not None:
+        result["precision"] = precision
     if not args.no_cpu_baseline:
         v, chains, wall, cpu = cpu_baseline(kind, B, N, args.cpu_sample, args.cpu_seconds)
         result["cpu_baseline"] = {

@@ -332,6 +332,8 @@ def test_low_precision_reported(cufk, device, dtype, N):
     rel = np.abs(diff).max() / np.abs(ref).max()
     print(f"{dtype} forward N={N}: rms {math.sqrt(np.mean(err_pos**2)):.3e}, max {np.abs(diff).max():.3e}, "
           f"rel max {rel:.2e}, rms at the last position {err_pos[-1]:.2e}")
+    marks = sorted({round(i * (N - 1) / 10) for i in range(11)})
+    print(f"{dtype} forward N={N}: rms by position " + ", ".join(f"{i}: {err_pos[i]:.1e}" for i in marks))
     ref_g = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"])
     gerr = [float(np.abs(gr.double().cpu().numpy() - rg).max() / np.abs(rg).max()) for gr, rg in zip(grads, ref_g)]
     print(f"{dtype} backward N={N}: rel max err (lengths, angles, dihedrals) " + ", ".join(f"{e:.2e}" for e in gerr))
