@@ -29,6 +29,11 @@ sample of chains of the same shape (chunks of about 128 x 2049 points until abou
 scaled to atoms/s.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss]
+                    [--graph]
+
+With --graph each input set's step is captured once in a HIP graph (torch.cuda.graph) and the
+timed steps replay the graphs: the kernels are the same, the per-step Python, autograd-engine and
+launch overhead is gone (which is what bounds small configs such as c1).
 """
 
 from __future__ import annotations
@@ -81,6 +86,8 @@ def parse_args():
     p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     p.add_argument("--kernel-reps", type=int, default=200)
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
+    p.add_argument("--graph", action="store_true",
+                   help="capture each input set's step (forward + torch.autograd.grad) in a HIP graph and time replays")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = about 15 s of work)")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -388,6 +395,25 @@ def main():
             fwds.append(fwd)
             bwds.append(bwd)
 
+    if args.graph:
+        # One graph per input set: warm up on a side stream, capture, then the timed steps
+        # replay (no per-step Python, autograd engine or launch overhead).
+        graphs = []
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for k in range(nsets):
+                for _ in range(3):
+                    steps[k]()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for k in range(nsets):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                steps[k]()
+            graphs.append(graph)
+        steps = [graph.replay for graph in graphs]
+
     for i in range(args.warmup):
         steps[i % nsets]()
     torch.cuda.synchronize()
@@ -408,7 +434,7 @@ def main():
     # backward node (autograd pre- and post-hooks on the output's grad_fn, run on the same
     # stream right before and after the node launches its kernel).  The extra event packets
     # cost a little per step, so this pass is reported apart from ms_per_step.
-    marks = [(ev(), ev(), ev(), ev()) for _ in range(args.steps)]
+    marks = [(ev(), ev(), ev(), ev()) for _ in range(0 if args.graph else args.steps)]
 
     def marker(m):
         def mark(out):
@@ -419,12 +445,12 @@ def main():
         return mark
 
     torch.cuda.synchronize()
-    for i in range(args.steps):
+    for i in range(len(marks)):
         marks[i][0].record(stream)
         steps[i % nsets](mark=marker(marks[i]))
     torch.cuda.synchronize()
-    seg_fwd = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
-    seg_bwd = sum(m[2].elapsed_time(m[3]) for m in marks) / args.steps
+    seg_fwd = sum(m[0].elapsed_time(m[1]) for m in marks) / len(marks) if marks else None
+    seg_bwd = sum(m[2].elapsed_time(m[3]) for m in marks) / len(marks) if marks else None
 
     # Kernel-level timing straight through the C ABI, rotating over the same sets.
     st = ctypes.c_void_p(stream.cuda_stream)
@@ -450,8 +476,12 @@ def main():
         precision = coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device)
 
     atoms = B * N
-    bw_bwd = bwd_bytes / (seg_bwd * 1e-3) / 1e9  # the backward kernel as the timed steps run it
-    bw_fwd = fwd_bytes / (seg_fwd * 1e-3) / 1e9
+    # The backward kernel as the timed steps run it; replayed graphs hold no events, so with
+    # --graph the C-ABI launches stand in.
+    bwd_ms = seg_bwd if seg_bwd is not None else t_bwd
+    fwd_ms = seg_fwd if seg_fwd is not None else t_fwd
+    bw_bwd = bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    bw_fwd = fwd_bytes / (fwd_ms * 1e-3) / 1e9
     traffic = MEASURED_TRAFFIC.get((args.config, f"{kind}_backward"))
     result = {
         "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
@@ -466,8 +496,9 @@ def main():
         "vs_baseline": None,
         "dtype": {"float32": "f32", "float64": "f64", "float16": "f16", "bfloat16": "bf16"}[dtype_name],
         "data": "synthetic",
-        "config": {"workload": f"{kind} fwd+bwd", "config": args.config, "batch": B, "points": N,
-                   "dtype": dtype_name, "anchors": "random", "input_sets": nsets},
+        "config": {"workload": f"{kind} fwd+bwd" + (", replayed HIP graph" if args.graph else ""),
+                   "config": args.config, "batch": B, "points": N, "dtype": dtype_name, "anchors": "random",
+                   "input_sets": nsets},
         "roofline": {
             "bound": "hbm",
             "kernel": f"{kind}_backward",
@@ -477,11 +508,11 @@ def main():
             "frac": bw_bwd / HBM_PEAK_GBS,
             "traffic": traffic,
             "algorithmic_bytes": bwd_bytes,
-            "avg_launch_us": seg_bwd * 1e3,
+            "avg_launch_us": bwd_ms * 1e3,
         },
         "kernels": {
-            "step_forward_us": seg_fwd * 1e3,
-            "step_backward_us": seg_bwd * 1e3,
+            "step_forward_us": seg_fwd * 1e3 if seg_fwd is not None else None,
+            "step_backward_us": seg_bwd * 1e3 if seg_bwd is not None else None,
             "step_forward_GBs": bw_fwd,
             "step_backward_GBs": bw_bwd,
             "abi_forward_us": t_fwd * 1e3,
