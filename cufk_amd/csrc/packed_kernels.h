@@ -233,8 +233,14 @@ __device__ __forceinline__ bool stage_params(const ParamRows<P, compute_t<T>>& r
 }
 
 // Lane-serial scan in double over the lane's steps (as forward_chain's): y[i] is the
-// translation of the lane-local prefix after item i.
-template <typename T, typename P, int K>
+// translation of the lane-local prefix after item i.  The hot instance runs every item
+// unguarded: items past the chain's last step read the next chain's slots of the flat rows (or
+// the rows' unused tail: lane runs end at most kCap + 1 elements into a chain's kCap + 2 slots)
+// and feed only positions that are never stored and the lane total of the chain's last lane,
+// which no lane of the chain consumes; the regularity tests mask them.  The instance with the
+// library sin/cos stays guarded (unguarded it needs more registers).  With Table, float angles
+// take sin/cos from the LDS table (table), otherwise from sin_cos_wide.
+template <typename T, typename P, int K, bool Table>
 __device__ __forceinline__ void packed_serial(const ParamRows<P, compute_t<T>>& rows, const PackedLane<P::kGroup, K>& ln,
                                               int points, const SinCosEntry* table, bool wide, Rigid<double>& q,
                                               compute_t<T> (&y)[K][3], bool& ok, compute_t<T>& lmin) {
@@ -242,37 +248,37 @@ __device__ __forceinline__ void packed_serial(const ParamRows<P, compute_t<T>>& 
   const int el = ln.c * (points - 1) + 2 + ln.s0;
   const int ea = ln.c * (points - 2) + 1 + ln.s0;
   const int ed = ln.c * (points - 3) + ln.s0;
-  auto run = [&]<bool Checked>() {
+  auto run = [&]<bool Checked, bool Guard>() {
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      if (i < ln.count) {
+      const bool in = i < ln.count;
+      if (!Guard || in) {
         const R l = rows.L[fslot<P::kStepGap>(el + i)];
         double s, c, S, C;
-        if constexpr (sizeof(R) == 4) {
-          if (table != nullptr) {
-            sin_cos_tab<Checked>(rows.A[fslot<P::kStepGap>(ea + i)], table, s, c);
-            sin_cos_tab<Checked>(rows.D[fslot<P::kStepGap>(ed + i)], table, S, C);
-          } else {
-            sin_cos_wide<Checked>(rows.A[fslot<P::kStepGap>(ea + i)], s, c);
-            sin_cos_wide<Checked>(rows.D[fslot<P::kStepGap>(ed + i)], S, C);
-          }
+        if constexpr (Table && sizeof(R) == 4) {
+          sin_cos_tab<Checked>(rows.A[fslot<P::kStepGap>(ea + i)], table, s, c);
+          sin_cos_tab<Checked>(rows.D[fslot<P::kStepGap>(ed + i)], table, S, C);
         } else {
           sin_cos_wide<Checked>(rows.A[fslot<P::kStepGap>(ea + i)], s, c);
           sin_cos_wide<Checked>(rows.D[fslot<P::kStepGap>(ed + i)], S, C);
         }
-        step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
-        ok = ok && l > R(0) && s >= FastPath<R>::kSinMin;
-        lmin = fmin(lmin, l);
+        if (i == 0)
+          step_first(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        else
+          step_forward(q.m, q.v, static_cast<double>(l), s, c, S, C);
+        ok = ok && (!in || (l > R(0) && s >= FastPath<R>::kSinMin));
+        lmin = in ? min_positive(lmin, l) : lmin;
       }
       y[i][0] = static_cast<R>(q.v[0]);
       y[i][1] = static_cast<R>(q.v[1]);
       y[i][2] = static_cast<R>(q.v[2]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   if (wide)
-    run.template operator()<true>();
+    run.template operator()<true, true>();
   else
-    run.template operator()<false>();
+    run.template operator()<false, false>();
 }
 
 // ---------------------------------------------------------------------------- forward
@@ -306,6 +312,14 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
   if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, 64 * W);
   wide = block_any<W>(wide, wide_vote, lane, wave);  // barrier: rows and table visible
 
+  Rigid<double> q = rigid_identity<double>();
+  R y[K][3];
+  bool ok = true;
+  R lmin = R(1.0e30);
+  packed_serial<T, P, K, sizeof(R) == 4>(rows, ln, points, sc_table, wide, q, y, ok, lmin);
+
+  // Each chain's first frame (block.cu:113-148), by its leader, after the lane scan: it is
+  // then not live across the scan, and the barrier below publishes it.
   FirstFrame<R> ff;
   if (ln.leader) {
     ff = first_frame<T>(rows.L[fslot<P::kStepGap>(ln.c * (points - 1))],
@@ -317,12 +331,6 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
     base[ln.c * 12 + 10] = ff.p2.y;
     base[ln.c * 12 + 11] = ff.p2.z;
   }
-
-  Rigid<double> q = rigid_identity<double>();
-  R y[K][3];
-  bool ok = true;
-  R lmin = R(1.0e30);
-  packed_serial<T, P, K>(rows, ln, points, sizeof(R) == 4 ? sc_table : nullptr, wide, q, y, ok, lmin);
   const Rigid<R> excl = group_exclusive<G>(narrow_rigid<R>(q), lane);
   __syncthreads();  // base published; every read of the parameter rows retired
 
@@ -645,7 +653,7 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
     R y[K][3];
     bool ok = true;
     R lmin = R(1.0e30);
-    packed_serial<T, P, K>(rows, ln, points, nullptr, wide, q, y, ok, lmin);
+    packed_serial<T, P, K, false>(rows, ln, points, nullptr, wide, q, y, ok, lmin);
     const Rigid<R> excl = group_exclusive<G>(narrow_rigid<R>(q), lane);
     __syncthreads();  // base published
     R Fm[9];
