@@ -341,16 +341,32 @@ def main():
             gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
 
             # The entry points the autograd path uses: the flagged forward and the backward
-            # that takes the forward's output (position-based adjoint for regular chains).
-            def fwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags):
-                rc = lib.cufk_reconstruct_fwd_flagged(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(flags),
-                                                      i64(B), i64(N), st)
-                assert rc == 0, rc
+            # that takes the forward's output (position-based adjoint for regular chains);
+            # float16/bfloat16 keep a float copy of the positions for it instead.
+            lib.cufk_reconstruct_shadow_floats.restype = i64
+            if s == 2 and lib.cufk_reconstruct_shadow_floats(i64(B), i64(N)) > 0:
+                pos = torch.empty(B, N, 3, device=device, dtype=torch.float32)
 
-            def bwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, g=g, gL=gL, gA=gA, gD=gD):
-                rc = lib.cufk_reconstruct_bwd_saved(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(flags),
-                                                    P(g), P(gL), P(gA), P(gD), i64(B), i64(N), st)
-                assert rc == 0, rc
+                def fwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, pos=pos, flags=flags):
+                    rc = lib.cufk_reconstruct_fwd_shadow(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz), P(pos),
+                                                         P(flags), i64(B), i64(N), st)
+                    assert rc == 0, rc
+
+                def bwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, pos=pos, flags=flags, g=g, gL=gL, gA=gA, gD=gD):
+                    rc = lib.cufk_reconstruct_bwd_shadow(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(pos), P(flags),
+                                                         P(g), P(gL), P(gA), P(gD), i64(B), i64(N), st)
+                    assert rc == 0, rc
+            else:
+
+                def fwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags):
+                    rc = lib.cufk_reconstruct_fwd_flagged(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz),
+                                                          P(flags), i64(B), i64(N), st)
+                    assert rc == 0, rc
+
+                def bwd(st, L=L, A=A, D=D, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, g=g, gL=gL, gA=gA, gD=gD):
+                    rc = lib.cufk_reconstruct_bwd_saved(code, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz),
+                                                        P(flags), P(g), P(gL), P(gA), P(gD), i64(B), i64(N), st)
+                    assert rc == 0, rc
 
             steps.append(step)
             fwds.append(fwd)

@@ -148,12 +148,33 @@ void check_status(int status, const char* what) {
 class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd> {
  public:
   static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
-                        Tensor p0, Tensor first_direction, Tensor initial_normal) {
+                        Tensor p0, Tensor first_direction, Tensor initial_normal, bool grad) {
     const Shape shape = check_geom(lengths, angles, dihedrals, true);
     const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
     const c10::DeviceGuard guard(lengths.device());
     check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
     Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
+    // grad: the call records a backward (grad mode on and a parameter row requiring grad).
+    const bool half = lengths.scalar_type() == torch::kFloat16 || lengths.scalar_type() == torch::kBFloat16;
+    const int64_t shadow_floats = half && grad ? cufk_reconstruct_shadow_floats(shape.batch, shape.points) : 0;
+    if (shadow_floats > 0) {
+      // float16/bfloat16 outputs are too coarse for the position-based adjoint: the forward
+      // keeps a float copy of the positions (12 bytes per point until the backward) and the
+      // backward runs over it instead of recomputing the chain.
+      Tensor positions = torch::empty({shape.batch, shape.points, 3}, lengths.options().dtype(torch::kFloat32));
+      Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
+      check_status(cufk_reconstruct_fwd_shadow(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
+                                               dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                                               a.initial_normal.data_ptr(), xyz.data_ptr(),
+                                               static_cast<float*>(positions.data_ptr()),
+                                               static_cast<uint8_t*>(regular.data_ptr()), shape.batch, shape.points,
+                                               current_stream(lengths)),
+                   "cufk_reconstruct_fwd_shadow");
+      ctx->saved_data["positions"] = positions;
+      ctx->saved_data["regular"] = regular;
+      return xyz;
+    }
     Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
     check_status(cufk_reconstruct_fwd_flagged(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
                                               dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
@@ -165,7 +186,6 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     // alias (no grad_fn, so no reference cycle; it shares the output's version counter): when
     // it is untouched at backward time, regular chains use the position-based adjoint;
     // if the caller modified it in place, every chain takes the exact recompute.
-    ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
     ctx->saved_data["xyz"] = xyz.detach();
     ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
     ctx->saved_data["regular"] = regular;
@@ -191,8 +211,19 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     Tensor grad_lengths = torch::empty_like(lengths);
     Tensor grad_angles = torch::empty_like(angles);
     Tensor grad_dihedrals = torch::empty_like(dihedrals);
-    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
     const Tensor regular = ctx->saved_data["regular"].toTensor();
+    if (ctx->saved_data.count("positions") != 0) {
+      const Tensor positions = ctx->saved_data["positions"].toTensor();
+      check_status(cufk_reconstruct_bwd_shadow(
+                       dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(),
+                       a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
+                       static_cast<const float*>(positions.data_ptr()), static_cast<const uint8_t*>(regular.data_ptr()),
+                       grad_points.data_ptr(), grad_lengths.data_ptr(), grad_angles.data_ptr(),
+                       grad_dihedrals.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
+                   "cufk_reconstruct_bwd_shadow");
+      return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
     if (xyz._version() == ctx->saved_data["xyz_version"].toInt()) {
       check_status(cufk_reconstruct_bwd_saved(
                        dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(),
@@ -208,13 +239,15 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
                                         grad_dihedrals.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
                    "cufk_reconstruct_bwd");
     }
-    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor()};
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
 
 Tensor apply_reconstruct(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
                          const Tensor& first_direction, const Tensor& initial_normal) {
-  return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal);
+  const bool grad = torch::GradMode::is_enabled() &&
+                    (lengths.requires_grad() || angles.requires_grad() || dihedrals.requires_grad());
+  return ReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal, grad);
 }
 
 // ------------------------------------------------------------------ anchor gradients

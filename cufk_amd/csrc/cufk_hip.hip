@@ -139,6 +139,59 @@ int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angle
   });
 }
 
+int64_t cufk_reconstruct_shadow_floats(int64_t batch, int64_t points) {
+  if (check_chain(batch, points) != CUFK_OK) return -1;
+  return use_shadow(batch, points - 3) ? batch * points * 3 : 0;
+}
+
+int cufk_reconstruct_fwd_shadow(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                const void* p0, const void* first_direction, const void* initial_normal, void* xyz,
+                                float* positions, uint8_t* chain_regular, int64_t batch, int64_t points,
+                                void* stream) {
+  if (dtype != CUFK_FLOAT16 && dtype != CUFK_BFLOAT16) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !xyz) return CUFK_ERR_NULL;
+  if (use_shadow(batch, points - 3) && (!positions || !chain_regular)) return CUFK_ERR_NULL;
+  const int N = static_cast<int>(points);
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      return shadow_fwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                                 cp<T>(initial_normal), mp<T>(xyz), positions, chain_regular, batch, N, st);
+    } else {
+      return static_cast<int>(CUFK_ERR_DTYPE);
+    }
+  });
+}
+
+int cufk_reconstruct_bwd_shadow(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                const void* p0, const void* first_direction, const void* initial_normal,
+                                const float* positions, const uint8_t* chain_regular, const void* grad_xyz,
+                                void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                                int64_t points, void* stream) {
+  if (dtype != CUFK_FLOAT16 && dtype != CUFK_BFLOAT16) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !grad_xyz || !grad_lengths ||
+      !grad_angles || !grad_dihedrals)
+    return CUFK_ERR_NULL;
+  if (use_shadow(batch, points - 3) && (!positions || !chain_regular)) return CUFK_ERR_NULL;
+  const int N = static_cast<int>(points);
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      return shadow_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                                 cp<T>(initial_normal), positions, chain_regular, cp<T>(grad_xyz), mp<T>(grad_lengths),
+                                 mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, N, st);
+    } else {
+      return static_cast<int>(CUFK_ERR_DTYPE);
+    }
+  });
+}
+
 int cufk_torsion_fwd(int dtype, const void* raw_pairs, int64_t raw_stride, const cufk_torsion_consts* consts, void* xyz,
                      int64_t batch, int64_t points, void* stream) {
   if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;

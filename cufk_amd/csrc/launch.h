@@ -31,6 +31,20 @@ constexpr int64_t kLongMaxGroups = int64_t{UINT32_MAX} / 256;
 
 inline int64_t long_segments(int64_t points, int64_t seg_steps) { return (points - 3 + seg_steps - 1) / seg_steps; }
 
+// Short chains: G lanes per chain, 8 steps per lane, several chains per workgroup (packed
+// kernels).  Measured on MI355X against one chain per workgroup: packing wins from about 4096
+// chains up (at 8192 chains: forward 9.5-15.5 us against 19-21 us for 9-128 steps), loses
+// below (fewer waves in flight), and its backward stops winning past 64 steps (at 128 steps
+// and 32768 chains: 44 us against 34 us).
+constexpr int kPackedFwdMaxSteps = 128;
+constexpr int kPackedBwdMaxSteps = 64;
+constexpr int64_t kPackedMinBatch = 4096;
+inline bool use_packed_fwd(int64_t B, int64_t steps) { return steps <= kPackedFwdMaxSteps && B >= kPackedMinBatch; }
+inline bool use_packed_bwd(int64_t B, int64_t steps) { return steps <= kPackedBwdMaxSteps && B >= kPackedMinBatch; }
+// Whether a float16/bfloat16 chain keeps float positions for its backward: wherever the
+// forward runs one chain per workgroup, so that the output is the plain forward's, bit for bit.
+inline bool use_shadow(int64_t B, int64_t steps) { return !use_packed_fwd(B, steps); }
+
 // ---------------------------------------------------------------------------- typed launchers
 // Each returns a cufk_status.  Pointers are device rows of B chains of N points; `anchor`
 // (optional) receives each chain's six anchor sums (F, tau) for anchor_grads_typed.
@@ -45,6 +59,17 @@ template <typename T>
 int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0,
                                     const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st,
                                     double* anchor = nullptr);
+
+// float16/bfloat16 forward that also keeps the positions in float (pos, B*N*3 floats) and the
+// chains' regularity flags, and the backward over them (position-based adjoint, exact
+// recompute for irregular chains).  Where use_shadow(B, N-3) is false the forward writes
+// neither pos nor regular and the backward recomputes the positions.
+template <typename T>
+int shadow_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, float* pos,
+                     uint8_t* regular, int64_t B, int N, hipStream_t st);
+template <typename T>
+int shadow_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const float* pos,
+                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st);
 
 // Backward over the saved forward output and its regularity flags (float and double only).
 template <typename T>

@@ -47,7 +47,8 @@
 #error "unknown CUFK_DTYPE"
 #endif
 // float32 and float64 keep the position-based backward over the saved output; float16 and
-// bfloat16 outputs are too coarse for it (FastPath<T>::kEnabled).
+// bfloat16 outputs are too coarse for it (FastPath<T>::kEnabled), and take it over a float
+// copy of their positions instead (shadow_*_typed).
 #define CUFK_SAVED_BACKWARD (CUFK_DTYPE == 0 || CUFK_DTYPE == 1)
 
 // Explicit instantiation of one launcher, its signature taken from its declaration.
@@ -99,14 +100,8 @@ template <typename Fn> int launch_chunks(int64_t batch, int threads, Fn&& fn) {
   return CUFK_OK;
 }
 
-// Short chains: G lanes per chain, 8 steps per lane, 64W/G chains per workgroup (packed
-// kernels).  Measured on MI355X against one chain per workgroup: packing wins from about 4096
-// chains up (at 8192 chains: forward 9.5-15.5 us against 19-21 us for 9-128 steps), loses
-// below (fewer waves in flight), and its backward stops winning past 64 steps (at 128 steps
-// and 32768 chains: 44 us against 34 us).
-constexpr int kPackedFwdMaxSteps = 128;
-constexpr int kPackedBwdMaxSteps = 64;
-constexpr int64_t kPackedMinBatch = 4096;
+// Packed plans (launch.h: when the packed kernels run): 64W/G chains per workgroup of
+// kPackedWaves waves.
 constexpr int kPackedWaves = 2;
 template <int MaxG = 16, typename Fn> int with_packed_plan(int steps, Fn&& fn) {
   if (steps <= 8) return fn.template operator()<1>();
@@ -116,8 +111,6 @@ template <int MaxG = 16, typename Fn> int with_packed_plan(int steps, Fn&& fn) {
   if constexpr (MaxG >= 16) return fn.template operator()<16>();
   return CUFK_ERR_STEPS;
 }
-inline bool use_packed_fwd(int64_t B, int steps) { return steps <= kPackedFwdMaxSteps && B >= kPackedMinBatch; }
-inline bool use_packed_bwd(int64_t B, int steps) { return steps <= kPackedBwdMaxSteps && B >= kPackedMinBatch; }
 // Launch a packed kernel over B chains, C per workgroup, in grid chunks that keep the grid's
 // work-item count within 32 bits.
 template <typename Fn> int launch_packed(int64_t B, int C, Fn&& fn) {
@@ -149,9 +142,23 @@ int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const
   });
 }
 
-// Backward without a saved output: the forward scan is rerun per chain, then the
+template <typename T>
+int shadow_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, float* pos,
+                     uint8_t* regular, int64_t B, int N, hipStream_t st) {
+  if (!use_shadow(B, N - 3)) return reconstruct_fwd_typed<T>(L, A, D, p0, fd, n0, xyz, nullptr, B, N, st);
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_forward_shadow_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
+                         pos + off * N * 3, regular + off, N);
+    });
+  });
+}
 
 CUFK_INSTANTIATE(reconstruct_fwd_typed<CUFK_T>)
+#if !CUFK_SAVED_BACKWARD
+CUFK_INSTANTIATE(shadow_fwd_typed<CUFK_T>)
+#endif
 
 }  // namespace cufk_amd
 #endif
@@ -174,8 +181,6 @@ int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T*
     });
   });
 }
-
-// Backward over the saved forward output: one launch, each chain taking the position-based
 
 CUFK_INSTANTIATE(reconstruct_bwd_recompute_typed<CUFK_T>)
 
@@ -202,6 +207,20 @@ int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0,
 }
 
 template <typename T>
+int shadow_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const float* pos,
+                     const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+  if (!use_shadow(B, N - 3)) return reconstruct_bwd_recompute_typed<T>(L, A, D, p0, fd, n0, g, gL, gA, gD, B, N, st);
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad, float>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, pos + off * N * 3,
+                         regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
+                         nullptr);
+    });
+  });
+}
+
+template <typename T>
 int anchor_grads_typed(const double* anchor, int64_t B, const T* fd, const T* n0, T* grad_p0, T* grad_fd, T* grad_n0,
                        hipStream_t st) {
   hipLaunchKernelGGL(anchor_gradients_kernel<T>, dim3(1), dim3(kAnchorThreads), 0, st, anchor, B, fd, n0, grad_p0,
@@ -211,6 +230,8 @@ int anchor_grads_typed(const double* anchor, int64_t B, const T* fd, const T* n0
 
 #if CUFK_SAVED_BACKWARD
 CUFK_INSTANTIATE(reconstruct_bwd_saved_typed<CUFK_T>)
+#else
+CUFK_INSTANTIATE(shadow_bwd_typed<CUFK_T>)
 #endif
 CUFK_INSTANTIATE(anchor_grads_typed<CUFK_T>)
 

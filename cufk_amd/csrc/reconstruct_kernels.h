@@ -173,15 +173,21 @@ __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const co
 //
 // Loss: *loss also receives sum_i |x_i - target_i|^2 over the chain's points (target: the
 // chain's (points, 3) row), from the positions as stored (rounded to T), accumulated in double.
-template <typename T, typename Lay, bool Segmented, bool Loss = false>
+//
+// Shadow (float16/bfloat16 whole chains): the positions are also stored unrounded, in float,
+// to shadow (the chain's (points, 3) row), and *regular receives the float32 chains' test
+// (FastPath<float>) on them, for the position-based backward over that copy.
+template <typename T, typename Lay, bool Segmented, bool Loss = false, bool Shadow = false>
 __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                               const T* __restrict__ Dr, const T* __restrict__ p0,
                                               const T* __restrict__ first_direction,
                                               const T* __restrict__ initial_normal, T* __restrict__ out,
                                               uint8_t* __restrict__ regular, int points, bool head,
                                               double* __restrict__ total, const T* __restrict__ target = nullptr,
-                                              T* __restrict__ loss = nullptr) {
+                                              T* __restrict__ loss = nullptr, float* __restrict__ shadow = nullptr) {
   using R = compute_t<T>;
+  static_assert(!Shadow || (!Segmented && !Loss && std::is_same_v<R, float>), "shadow rows: whole half-type chains");
+  using Fast = std::conditional_t<Shadow, FastPath<R>, FastPath<T>>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
   constexpr int kStage = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
@@ -233,7 +239,8 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       else
         lane_scan<T, K, false, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
-      lane_scan_chain<T, K, kTable, true>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok, lmin);
+      lane_scan_chain<T, K, kTable, true, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
+                                                lmin);
     }
   }
 
@@ -310,7 +317,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       stage[6] = ff.p2.x; stage[7] = ff.p2.y; stage[8] = ff.p2.z;
     }
   }
-  if constexpr (FastPath<T>::kEnabled) {
+  if constexpr (Fast::kEnabled) {
     if (regular != nullptr) {
       const bool wave_ok = __all(ok);
       const R wmin = wave_min(lmin);
@@ -325,8 +332,8 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   __syncthreads();
   if (regular != nullptr && tid == 0) {
     bool reg = false;
-    if constexpr (FastPath<T>::kEnabled) {
-      reg = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= FastPath<T>::kSinMin;
+    if constexpr (Fast::kEnabled) {
+      reg = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= Fast::kSinMin;
       R m = fmin(ff.L0, ff.L1);
       R x = abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2);
 #pragma unroll
@@ -335,7 +342,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         m = fmin(m, wave_stat[w][1]);
         x = fmax(x, wave_stat[w][2]);
       }
-      reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * m;
+      reg = reg && x <= static_cast<R>(Fast::kScale) * m;
     }
     *regular = reg ? 1 : 0;
   }
@@ -353,6 +360,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     }
   }
   store_point_row<Lay>(out, stage, points, tid, !Segmented || head);
+  if constexpr (Shadow) store_point_row<Lay>(shadow, stage, points, tid);
 }
 
 template <typename T, int W, int K, int Pad = 4>
@@ -365,6 +373,21 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
                                              dihedrals + row * (points - 3), p0, first_direction, initial_normal,
                                              xyz + row * points * 3, regular != nullptr ? regular + row : nullptr,
                                              points, true, nullptr);
+}
+
+// The forward of a float16/bfloat16 chain that also keeps its positions in float (shadow, a
+// (B, N, 3) float array) and flags the chains whose backward may take the position-based
+// adjoint over them.
+template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_forward_shadow_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    T* __restrict__ xyz, float* __restrict__ shadow, uint8_t* __restrict__ regular, int points) {
+  const int64_t row = blockIdx.x;
+  forward_chain<T, Layout<W, K, Pad>, false, false, true>(
+      lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0, first_direction,
+      initial_normal, xyz + row * points * 3, regular + row, points, true, nullptr, nullptr, nullptr,
+      shadow + row * points * 3);
 }
 
 // ============================================================================ exact backward
@@ -657,16 +680,21 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
   }
 }
 
-template <typename T, typename Lay>
-__device__ __forceinline__ void position_chain(const T* __restrict__ Xr, const T* __restrict__ Gr,
+// Positions Xr of element type P: the chain's own output (P = T), or the float copy a
+// float16/bfloat16 forward kept (P = float).
+template <typename T, typename Lay, typename P = T>
+__device__ __forceinline__ void position_chain(const P* __restrict__ Xr, const T* __restrict__ Gr,
                                                T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                compute_t<T>* xs, compute_t<T>* gs,
                                                compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
                                                double* __restrict__ anchor = nullptr) {
-  {
+  static_assert(std::is_same_v<compute_t<P>, compute_t<T>>, "positions in the compute type");
+  if constexpr (std::is_same_v<P, T>) {
     compute_t<T>* const dst[2] = {xs, gs};
     const T* const src[2] = {Xr, Gr};
     load_point_rows<Lay, 2>(dst, src, points, threadIdx.x);
+  } else {
+    load_point_rows_pair<Lay>(xs, Xr, gs, Gr, points, threadIdx.x);
   }
   __syncthreads();
   position_adjoint<T, Lay>(gLr, gAr, gDr, xs, gs, wave_sum, points, anchor);
@@ -816,12 +844,13 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_recompute_kernel(
 // Backward given the forward's own output: one workgroup per chain, the position-based
 // adjoint for chains with regular[row] != 0 and the exact recompute for the others, in one
 // launch.  The two paths share the LDS: region A holds xs or the parameter rows, region B
-// the gradient row.
-template <typename T, int W, int K, int Pad>
+// the gradient row.  P = float reads the float positions a float16/bfloat16 forward kept
+// (reconstruct_forward_shadow_kernel) in place of its output.
+template <typename T, int W, int K, int Pad, typename P = T>
 __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
-    const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
+    const P* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
     T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points,
     double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
@@ -838,8 +867,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
   T* gAr = grad_angles + row * (points - 2);
   T* gDr = grad_dihedrals + row * (points - 3);
   if (regular[row] != 0) {
-    position_chain<T, Lay>(xyz + row * points * 3, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a, region_b,
-                           wave_sum, points, an);
+    position_chain<T, Lay, P>(xyz + row * points * 3, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a, region_b,
+                              wave_sum, points, an);
   } else {
     exact_chain<T, Lay>(lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0,
                         first_direction, initial_normal, grad_xyz + row * points * 3, gLr, gAr, gDr, region_a,

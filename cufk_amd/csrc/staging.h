@@ -115,24 +115,25 @@ template <typename Lay, typename V, typename S> __device__ __forceinline__ V lds
   }
 }
 
-// Rows of NR arrays into LDS: dst[r][slot(first + e)] = src[r][first + e] for e in [0, n).
-// Two-phase: every global load of the thread is issued into registers before the first LDS
-// write, so a workgroup pays one memory latency per staging phase, not one per group.
-// MaxN bounds n at compile time.  A 16-byte group never straddles a lane segment, so its
-// elements land in consecutive slots; Vec writes it with one vector LDS store (slots 16-byte
-// aligned), otherwise element by element.  Returns whether any element this thread staged
-// from a row in RangeRows (bit r for row r) lies beyond the polynomial range of
-// sin_cos_wide.
-template <int NR, int MaxN, int Lanes, bool Vec, unsigned RangeRows = 0, typename T, typename SlotFn>
-__device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
-                                           int tid, SlotFn slot) {
+// One thread's share of NR rows moved into LDS, in two phases: fetch() issues the thread's
+// global loads of src[r][first, first + n) into registers; commit() writes them to
+// dst[r][slot(first + e)] and returns whether any element of a row in RangeRows (bit r for
+// row r) lies beyond the polynomial range of sin_cos_wide.  MaxN bounds n at compile time.
+// A 16-byte group never straddles a lane segment, so its elements land in consecutive slots;
+// Vec writes it with one vector LDS store (slots 16-byte aligned), otherwise element by
+// element.
+template <int NR, int MaxN, int Lanes, typename T, bool Half = sizeof(T) == 2> struct RowFetch {  // float, double
   using R = compute_t<T>;
-  if constexpr (Unit<T>::kElems > 1) {
-    constexpr int E = Unit<T>::kElems;
-    constexpr int kPer = (MaxN / E + Lanes - 1) / Lanes;
-    typename Unit<T>::Local buf[NR][kPer];
-    R tail[NR];
-    const int groups = n / E;
+  static constexpr int E = Unit<T>::kElems;
+  static constexpr int kPer = (MaxN / E + Lanes - 1) / Lanes;
+  typename Unit<T>::Local buf[NR][kPer];
+  R tail[NR];
+  int first, n, groups, te;
+
+  __device__ __forceinline__ void fetch(const T* const (&src)[NR], int first_, int n_, int tid) {
+    first = first_;
+    n = n_;
+    groups = n / E;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int g = tid + j * Lanes;
@@ -141,11 +142,15 @@ __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const
         for (int r = 0; r < NR; ++r) buf[r][j] = *reinterpret_cast<const typename Unit<T>::Global*>(src[r] + first + E * g);
       }
     }
-    const int te = E * groups + tid;  // at most E-1 tail elements, one per low thread
+    te = E * groups + tid;  // at most E-1 tail elements, one per low thread
     if (te < n) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) tail[r] = src[r][first + te];
     }
+  }
+
+  template <bool Vec, unsigned RangeRows, typename SlotFn>
+  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid, SlotFn slot) const {
     bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -175,10 +180,19 @@ __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const
       }
     }
     return wide;
-  } else if constexpr (sizeof(T) == 2) {
-    constexpr int kPer = (MaxN / 8 + 1 + Lanes - 1) / Lanes;  // a misaligned row spans one more window
-    u16x8 buf[NR][kPer];
-    int lead[NR], windows[NR];
+  }
+};
+
+// float16/bfloat16 rows move in 16-byte windows (above).
+template <int NR, int MaxN, int Lanes, typename T> struct RowFetch<NR, MaxN, Lanes, T, true> {
+  using R = compute_t<T>;
+  static constexpr int kPer = (MaxN / 8 + 1 + Lanes - 1) / Lanes;  // a misaligned row spans one more window
+  u16x8 buf[NR][kPer];
+  int first, n, lead[NR], windows[NR];
+
+  __device__ __forceinline__ void fetch(const T* const (&src)[NR], int first_, int n_, int tid) {
+    first = first_;
+    n = n_;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       lead[r] = window_lead(src[r] + first);
@@ -191,6 +205,10 @@ __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const
       for (int r = 0; r < NR; ++r)
         if (g < windows[r]) buf[r][j] = *reinterpret_cast<const u16x8*>(src[r] + first - lead[r] + 8 * g);
     }
+  }
+
+  template <bool Vec, unsigned RangeRows, typename SlotFn>
+  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid, SlotFn slot) const {
     bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -213,31 +231,20 @@ __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const
       }
     }
     return wide;
-  } else {
-    constexpr int kPer = (MaxN + Lanes - 1) / Lanes;
-    R buf[NR][kPer];
-    bool wide = false;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = tid + j * Lanes;
-      if (e < n) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) buf[r][j] = widen(src[r][first + e]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = tid + j * Lanes;
-      if (e < n) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          dst[r][slot(first + e)] = buf[r][j];
-          if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(buf[r][j]);
-        }
-      }
-    }
-    return wide;
   }
+};
+
+// Rows of NR arrays into LDS: dst[r][slot(first + e)] = src[r][first + e] for e in [0, n).
+// Every global load of the thread is issued into registers before the first LDS write, so a
+// workgroup pays one memory latency per staging phase, not one per group.  Returns whether
+// any element this thread staged from a row in RangeRows lies beyond the polynomial range of
+// sin_cos_wide (RowFetch).
+template <int NR, int MaxN, int Lanes, bool Vec, unsigned RangeRows = 0, typename T, typename SlotFn>
+__device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
+                                           int tid, SlotFn slot) {
+  RowFetch<NR, MaxN, Lanes, T> rows;
+  rows.fetch(src, first, n, tid);
+  return rows.template commit<Vec, RangeRows>(dst, tid, slot);
 }
 
 // NR step rows (n <= kCap elements each) into step layouts; see stage_rows for RangeRows.
@@ -257,6 +264,29 @@ __device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], 
   }
   stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, 0u, T>(dst, src, 9, 3 * points - 9, tid,
                                                            [](int e) { return Lay::point_slot(e); });
+}
+
+// Two (points, 3) rows of different element types (float positions, the gradients of a
+// float16/bfloat16 chain) into point layouts, both rows' global loads issued before the first
+// LDS write.
+template <typename Lay, typename TA, typename TB>
+__device__ __forceinline__ void load_point_rows_pair(compute_t<TA>* da, const TA* __restrict__ sa, compute_t<TB>* db,
+                                                     const TB* __restrict__ sb, int points, int tid) {
+  if (tid < 9) {
+    da[tid] = widen(sa[tid]);
+    db[tid] = widen(sb[tid]);
+  }
+  auto slot = [](int e) { return Lay::point_slot(e); };
+  const TA* const src_a[1] = {sa};
+  const TB* const src_b[1] = {sb};
+  compute_t<TA>* const dst_a[1] = {da};
+  compute_t<TB>* const dst_b[1] = {db};
+  RowFetch<1, 3 * Lay::kCap, Lay::kLanes, TA> a;
+  RowFetch<1, 3 * Lay::kCap, Lay::kLanes, TB> b;
+  a.fetch(src_a, 9, 3 * points - 9, tid);
+  b.fetch(src_b, 9, 3 * points - 9, tid);
+  a.template commit<Lay::kVec, 0u>(dst_a, tid, slot);
+  b.template commit<Lay::kVec, 0u>(dst_b, tid, slot);
 }
 
 // One lane's run of n <= N consecutive elements between global memory and registers, in

@@ -107,6 +107,35 @@ int cufk_reconstruct_bwd_saved(int dtype, const void* lengths, const void* angle
                                void* grad_angles, void* grad_dihedrals, int64_t batch, int64_t points, void* stream);
 
 /*
+ * float16/bfloat16 forward and backward over a float copy of the positions.  No reference
+ * counterpart: the reference's backward (block.cu:331-365) recomputes from the saved inputs.
+ * Half-precision outputs are too coarse for the position-based adjoint that float32 and
+ * float64 run over their saved output (cufk_reconstruct_bwd_saved), so cufk_reconstruct_bwd
+ * reruns the forward scan for them; these two replace that rerun by a float copy kept by the
+ * forward, at 12 bytes per point of extra memory between the two calls.
+ *
+ * cufk_reconstruct_shadow_floats(batch, points): the number of floats `positions` must hold,
+ * batch*points*3, or 0 where the forward packs short chains several per workgroup (batch >=
+ * 4096 and points <= 131): there the forward writes neither positions nor chain_regular, the
+ * backward recomputes the positions, and both may be NULL.  -1 for invalid shapes.
+ *
+ * cufk_reconstruct_fwd_shadow: xyz exactly as cufk_reconstruct_fwd writes it, plus the
+ * unrounded float positions (B, N, 3) and chain_regular (B,) under the float32 test of
+ * cufk_reconstruct_fwd_flagged.  cufk_reconstruct_bwd_shadow: what cufk_reconstruct_bwd
+ * computes, from positions and chain_regular as the forward wrote them for the same inputs.
+ * Other dtypes: CUFK_ERR_DTYPE.
+ */
+int64_t cufk_reconstruct_shadow_floats(int64_t batch, int64_t points);
+int cufk_reconstruct_fwd_shadow(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                const void* p0, const void* first_direction, const void* initial_normal, void* xyz,
+                                float* positions, uint8_t* chain_regular, int64_t batch, int64_t points, void* stream);
+int cufk_reconstruct_bwd_shadow(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                const void* p0, const void* first_direction, const void* initial_normal,
+                                const float* positions, const uint8_t* chain_regular, const void* grad_xyz,
+                                void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                                int64_t points, void* stream);
+
+/*
  * Torsion-only forward from raw interleaved (sin, cos) pairs, raw row b at
  * raw + b*raw_stride (elements), 2*(N-3) values per row.  xyz (B, N, 3) dense.
  * Replaces torsion.cu:387-397 and forward_kernel (torsion.cu:254-295).

@@ -35,6 +35,10 @@ def lib():
     for name in ("cufk_long_state_doubles", "cufk_long_work_doubles"):
         getattr(lib, name).argtypes = [i64, i64, i64]
         getattr(lib, name).restype = i64
+    lib.cufk_reconstruct_shadow_floats.argtypes = [i64, i64]
+    lib.cufk_reconstruct_shadow_floats.restype = i64
+    lib.cufk_reconstruct_fwd_shadow.argtypes = [ctypes.c_int] + [vp] * 9 + [i64, i64, vp]
+    lib.cufk_reconstruct_bwd_shadow.argtypes = [ctypes.c_int] + [vp] * 12 + [i64, i64, vp]
     lib.cufk_long_segment_steps.argtypes = [i64, i64]
     lib.cufk_long_segment_steps.restype = i64
     lib.cufk_error_string.restype = ctypes.c_char_p
@@ -57,12 +61,15 @@ def test_header_declares_the_entry_points():
         "cufk_reconstruct_bwd",
         "cufk_reconstruct_bwd_anchored",
         "cufk_reconstruct_bwd_saved",
+        "cufk_reconstruct_bwd_shadow",
         "cufk_reconstruct_fwd",
         "cufk_reconstruct_fwd_flagged",
+        "cufk_reconstruct_fwd_shadow",
         "cufk_reconstruct_long_bwd",
         "cufk_reconstruct_long_fwd",
         "cufk_reconstruct_loss_bwd",
         "cufk_reconstruct_loss_fwd",
+        "cufk_reconstruct_shadow_floats",
         "cufk_torsion_bwd",
         "cufk_torsion_fwd",
         "cufk_version",
@@ -113,6 +120,34 @@ def test_reconstruct_status_paths(lib):
     assert bs(0, p, p, p, p, p, p, p, null, p, p, p, p, 4, 10, null) == ERR_NULL  # flags are required
     assert bs(0, p, p, p, p, p, p, p, p, p, p, p, p, 4, 3, null) == ERR_POINTS
     assert bs(0, p, p, p, p, p, p, p, p, p, p, p, p, 0, 10, null) == OK
+
+
+def test_shadow_sizes_and_status_paths(lib):
+    n = lib.cufk_reconstruct_shadow_floats
+    assert n(16384, 1026) == 16384 * 1026 * 3
+    assert n(4095, 100) == 4095 * 100 * 3  # below the packed batch: one chain per workgroup
+    assert n(4096, 131) == 0 and n(131072, 64) == 0  # packed forward: the backward recomputes
+    assert n(4096, 132) == 4096 * 132 * 3
+    assert n(0, 10) == 0
+    assert n(4, 3) == -1 and n(4, 2052) == -1 and n(-1, 10) == -1
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_fwd_shadow
+    #        dtype L  A  D  p0 d0 n0 xyz pos flags
+    for dtype in (0, 1, 9):  # float32 and float64 keep their own output
+        assert f(dtype, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(3, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert f(3, p, p, p, p, p, p, p, null, p, 4, 10, null) == ERR_NULL  # positions are written
+    assert f(2, p, p, p, p, p, p, p, p, null, 4, 10, null) == ERR_NULL  # and flags
+    assert f(3, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL
+    assert f(3, p, p, p, p, p, p, p, null, null, 0, 10, null) == OK
+    b = lib.cufk_reconstruct_bwd_shadow
+    #        dtype L  A  D  p0 d0 n0 pos flags g  gL gA gD
+    assert b(0, p, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert b(2, p, p, p, p, p, p, null, p, p, p, p, p, 4, 10, null) == ERR_NULL
+    assert b(2, p, p, p, p, p, p, p, p, null, p, p, p, 4, 10, null) == ERR_NULL
+    assert b(3, p, p, p, p, p, p, p, p, p, p, p, p, 4, 3, null) == ERR_POINTS
+    assert b(3, p, p, p, p, p, p, null, null, p, p, p, p, 0, 10, null) == OK
 
 
 def test_torsion_status_paths(lib):

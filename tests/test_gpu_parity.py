@@ -423,6 +423,10 @@ def _abi():
     lib.cufk_reconstruct_fwd_flagged.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_reconstruct_bwd.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
     lib.cufk_reconstruct_bwd_saved.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_reconstruct_shadow_floats.argtypes = [i64, i64]
+    lib.cufk_reconstruct_shadow_floats.restype = i64
+    lib.cufk_reconstruct_fwd_shadow.argtypes = [ctypes.c_int] + [vp] * 9 + [i64, i64, vp]
+    lib.cufk_reconstruct_bwd_shadow.argtypes = [ctypes.c_int] + [vp] * 12 + [i64, i64, vp]
     return lib
 
 
@@ -524,6 +528,163 @@ def test_mixed_regular_and_irregular_batch(cufk, device):
         err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
         print("per-chain rel err", err)
         assert err.max() <= 2e-4
+
+
+# ----------------------------------------------------------------- half types: float positions
+
+
+def _shadow_forward(lib, L, A, D, an):
+    """cufk_reconstruct_fwd_shadow; positions and flags are None where the library keeps none."""
+    B, N = L.shape[0], L.shape[1] + 1
+    xyz = torch.empty(B, N, 3, device=L.device, dtype=L.dtype)
+    n = lib.cufk_reconstruct_shadow_floats(B, N)
+    assert n in (0, B * N * 3)
+    pos = torch.full((B, N, 3), float("nan"), device=L.device) if n else None
+    reg = torch.full((B,), 7, device=L.device, dtype=torch.uint8) if n else None
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = lib.cufk_reconstruct_fwd_shadow(_CODES[L.dtype], p(L), p(A), p(D), *map(p, an), p(xyz), p(pos), p(reg), B, N,
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    return xyz, pos, reg
+
+
+def _shadow_backward(lib, L, A, D, an, pos, reg, g):
+    B, N = L.shape[0], L.shape[1] + 1
+    out = [torch.empty_like(t) for t in (L, A, D)]
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = lib.cufk_reconstruct_bwd_shadow(_CODES[L.dtype], p(L), p(A), p(D), *map(p, an), p(pos), p(reg), p(g),
+                                         *map(p, out), B, N, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_shadow_forward_positions_and_flags(cufk, device, dtype):
+    """The half-type forward that keeps float positions: its output equals the plain forward's
+    bit for bit, the kept positions round to exactly that output, they match the float64
+    oracle to float32 accuracy, and the flags follow the float32 regularity test (the cases of
+    test_regularity_flags: negative bond, small angle inside and at the first frame, zero bond)."""
+    lib = _abi()
+    d = _inputs(6, 300, seed=21, anchors=True, dtype=dtype)
+    d["lengths"][1, 7] = -d["lengths"][1, 7]
+    d["angles"][2, 40] = _round(0.2, dtype)
+    d["angles"][3, 0] = _round(math.pi - 0.2, dtype)
+    d["lengths"][4, 1] = 0.0
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    an = _anchors3(d, dtype, device)
+    xyz, pos, reg = _shadow_forward(lib, L, A, D, an)
+    plain, _ = _flagged_forward(lib, L, A, D, an)
+    torch.cuda.synchronize()
+    assert torch.equal(xyz, plain)
+    assert torch.equal(pos.to(dtype), xyz)
+    assert reg.cpu().tolist() == [1, 0, 0, 0, 0, 1]
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    err = np.abs(pos.double().cpu().numpy() - ref).max()
+    print(f"{dtype} shadow positions: max abs err {err:.2e} nm against float64 on the same inputs")
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [4, 5, 70, 259, 1028, 2049, 2051])
+def test_shadow_backward_is_the_float32_adjoint(cufk, device, dtype, N):
+    """Over the kept float positions the half-type backward runs the float32 position-based
+    adjoint on the same values: it equals cufk_reconstruct_bwd_saved at float32 (positions as
+    xyz, the gradient widened exactly), rounded to the dtype, bit for bit.  Against the float64
+    oracle on the rounded inputs it holds the low-precision sanity bound (3e-2 relative)."""
+    lib = _abi()
+    B = 4
+    d = _inputs(B, N, seed=300 + N, anchors=True, dtype=dtype)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    _, pos, reg = _shadow_forward(lib, L, A, D, an)
+    assert reg.cpu().tolist() == [1] * B
+    got = _shadow_backward(lib, L, A, D, an, pos, reg, g)
+    f32 = [t.float() for t in (L, A, D)]
+    an32 = [t.float() for t in an]
+    want = [torch.empty_like(t) for t in f32]
+    p = lambda t: t.data_ptr()  # noqa: E731
+    assert lib.cufk_reconstruct_bwd_saved(0, *map(p, f32), *map(p, an32), p(pos), p(reg), p(g.float()), *map(p, want),
+                                          B, N, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    for a, w in zip(got, want):
+        assert torch.equal(a, w.to(dtype))
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for a, r in zip(got, ref):
+        assert np.abs(a.double().cpu().numpy() - r).max() <= 3e-2 * max(1e-30, np.abs(r).max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_shadow_backward_irregular_chains_recompute(cufk, device, dtype):
+    """Chains the forward flags irregular take the exact recompute inside the same launch: their
+    gradients equal cufk_reconstruct_bwd's bit for bit; every chain stays within the
+    low-precision bound of the oracle."""
+    lib = _abi()
+    B, N = 8, 600
+    d = _inputs(B, N, seed=24, anchors=True, dtype=dtype)
+    d["lengths"][2, 100] *= -1
+    d["angles"][5, 300] = _round(0.1, dtype)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    _, pos, reg = _shadow_forward(lib, L, A, D, an)
+    assert reg.cpu().tolist() == [1, 1, 0, 1, 1, 0, 1, 1]
+    got = _shadow_backward(lib, L, A, D, an, pos, reg, g)
+    exact = [torch.empty_like(t) for t in (L, A, D)]
+    p = lambda t: t.data_ptr()  # noqa: E731
+    assert lib.cufk_reconstruct_bwd(_CODES[dtype], p(L), p(A), p(D), *map(p, an), p(g), *map(p, exact), B, N,
+                                    torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    for a, e in zip(got, exact):
+        assert torch.equal(a[[2, 5]], e[[2, 5]])
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for a, r in zip(got, ref):
+        err = np.abs(a.double().cpu().numpy() - r).max(axis=1) / np.abs(r).max(axis=1)
+        print(f"{dtype} per-chain rel err", err)
+        assert err.max() <= 3e-2
+
+
+def test_shadow_short_chains_in_large_batches_recompute(cufk, device):
+    """Where the forward packs short chains (4096 chains of 100 points) the library keeps no
+    float positions: the shadow forward writes the plain forward's output and the shadow
+    backward, given NULL positions and flags, equals cufk_reconstruct_bwd bit for bit."""
+    lib = _abi()
+    dtype, B, N = torch.bfloat16, 4096, 100
+    d = _inputs(B, N, seed=26, anchors=True, dtype=dtype)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    xyz, pos, reg = _shadow_forward(lib, L, A, D, an)
+    assert pos is None and reg is None
+    plain, _ = _flagged_forward(lib, L, A, D, an)
+    got = _shadow_backward(lib, L, A, D, an, None, None, g)
+    exact = [torch.empty_like(t) for t in (L, A, D)]
+    p = lambda t: t.data_ptr()  # noqa: E731
+    assert lib.cufk_reconstruct_bwd(_CODES[dtype], p(L), p(A), p(D), *map(p, an), p(g), *map(p, exact), B, N,
+                                    torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(xyz, plain)
+    for a, e in zip(got, exact):
+        assert torch.equal(a, e)
+
+
+def test_half_autograd_takes_the_float_positions(cufk, device):
+    """bfloat16 autograd: the step's gradients are those of the shadow entry points; without
+    gradients the forward is the plain one."""
+    lib = _abi()
+    dtype, B, N = torch.bfloat16, 16, 1026
+    d = _inputs(B, N, seed=27, anchors=True, dtype=dtype)
+    xyz, grads = _run(cufk, d, dtype, device)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    g = _dev(d["grad"], dtype, device)
+    an = _anchors3(d, dtype, device)
+    sx, pos, reg = _shadow_forward(lib, L, A, D, an)
+    want = _shadow_backward(lib, L, A, D, an, pos, reg, g)
+    nograd, _ = _run(cufk, d, dtype, device, grad=False)
+    torch.cuda.synchronize()
+    assert torch.equal(xyz, sx) and torch.equal(nograd, sx)
+    for a, w in zip(grads, want):
+        assert torch.equal(a, w)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
