@@ -33,6 +33,7 @@ template <int W, int K, int Pad = 4> struct Layout {
   static_assert(Pad == 4 || Pad == 1, "padding is 4 words (vector LDS access) or 1 word");
   static constexpr int kWaves = W;
   static constexpr int kItems = K;
+  static constexpr int kPad = Pad;
   static constexpr int kLanes = 64 * W;
   static constexpr int kCap = kLanes * K;  // steps per chain
   static constexpr bool kVec = Pad == 4;    // lane runs 16-byte aligned
@@ -50,6 +51,47 @@ template <int W, int K, int Pad = 4> struct Layout {
   __device__ __forceinline__ static int lane_point_base(int tid) { return 12 + tid * kPointStride; }
 };
 
+// Where the elements x of a row live in LDS.  slot(x) gives one slot; run(x) gives slot(x) and
+// x's offset within its lane segment (kSeg elements), from which run_slot gives the slots of
+// the following elements (kStride apart, plus the layout's padding for each segment end
+// crossed) without a division per element.
+struct SlotRun {
+  int slot;
+  int off;
+};
+template <typename Lay> struct StepRowMap {  // step rows: element s at step_slot(s)
+  static constexpr int kSeg = Lay::kItems;
+  static constexpr int kStride = 1;
+  static constexpr int kPad = Lay::kPad;
+  __device__ __forceinline__ static int slot(int s) { return Lay::step_slot(s); }
+  __device__ __forceinline__ static SlotRun run(int s) { return {Lay::step_slot(s), s % kSeg}; }
+};
+template <typename Lay> struct PointRowMap {  // flat (points, 3) rows, elements x >= 9
+  static constexpr int kSeg = 3 * Lay::kItems;
+  static constexpr int kStride = 1;
+  static constexpr int kPad = Lay::kPad;
+  __device__ __forceinline__ static int slot(int x) { return Lay::point_slot(x); }
+  __device__ __forceinline__ static SlotRun run(int x) {
+    const int t = x - 9;
+    const int q = t / kSeg;
+    return {12 + t + kPad * q, t - q * kSeg};
+  }
+};
+template <typename Lay> struct StepPointMap {  // step s at the first point slot of point s+3
+  static constexpr int kSeg = Lay::kItems;
+  static constexpr int kStride = 3;
+  static constexpr int kPad = Lay::kPad;
+  __device__ __forceinline__ static int slot(int s) { return Lay::point_slot(9 + 3 * s); }
+  __device__ __forceinline__ static SlotRun run(int s) { return {Lay::point_slot(9 + 3 * s), s % kSeg}; }
+};
+// Slot of element x + k, for r = Map::run(x) and 0 <= k < 8.
+template <typename Map> __device__ __forceinline__ int run_slot(SlotRun r, int k) {
+  if constexpr (Map::kSeg >= 8)  // at most one segment end within 8 elements
+    return r.slot + Map::kStride * k + (r.off + k >= Map::kSeg ? Map::kPad : 0);
+  else
+    return r.slot + Map::kStride * k + Map::kPad * ((r.off + k) / Map::kSeg);
+}
+
 // 16-byte global access unit for T: 4 floats or 2 doubles (dword-aligned rows suffice);
 // float16/bfloat16 rows are only 2-byte aligned and move in windows (below).
 template <typename T> struct Unit {
@@ -66,39 +108,46 @@ template <> struct Unit<double> {
   typedef f64x2 Local;
 };
 
-// float16/bfloat16 rows in 16-byte windows aligned down from the row start: window g covers
-// the row's elements 8g - lead .. 8g - lead + 7, lead being the row start's element offset in
-// its 16-byte block.  A load may read bytes of the first and last window that lie outside the
-// row; they share a 16-byte block, hence a page, with bytes of the row, and are discarded.
-// Stores write whole windows only inside the row and single elements at its two ends, so
-// rows written by other workgroups are never touched.
+// float16/bfloat16 rows are only 2-byte aligned.  A row of n elements splits at its 16-byte
+// block boundaries: `head` elements before the first boundary, `windows` whole 16-byte windows
+// of 8 elements, and `tail` elements after the last boundary (head, tail <= 7).  Windows move
+// as one 16-byte access each, head and tail elements one per thread, so no access touches
+// bytes outside the row.
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-template <typename T> __device__ __forceinline__ int window_lead(const T* p) {
+struct HalfSplit {
+  int head;
+  int windows;
+  int tail;
+};
+template <typename T> __device__ __forceinline__ HalfSplit half_split(const T* row, int n) {
   static_assert(sizeof(T) == 2, "windows are for 2-byte elements");
-  return static_cast<int>((reinterpret_cast<uintptr_t>(p) >> 1) & 7);
+  const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(row) >> 1) & 7);
+  const int head = min((8 - lead) & 7, max(n, 0));
+  const int windows = (max(n, 0) - head) >> 3;
+  return {head, windows, max(n, 0) - head - 8 * windows};
 }
-template <typename T> __device__ __forceinline__ int window_count(int n, int lead) { return n > 0 ? (n + lead + 7) >> 3 : 0; }
 
-// dst[e] = val(e) for e in [0, n), by the Lanes threads of a workgroup.
-template <int Lanes, typename T, typename ValFn>
-__device__ __forceinline__ void store_windows(T* __restrict__ dst, int n, int tid, ValFn val) {
-  const int lead = window_lead(dst);
-  const int windows = window_count<T>(n, lead);
-  for (int g = tid; g < windows; g += Lanes) {
-    const int e0 = 8 * g - lead;
-    if (e0 >= 0 && e0 + 8 <= n) {
-      u16x8 v;
+// dst[e] = src[Map::slot(x0 + e)] rounded to T, for e in [0, n), by the Lanes threads of a
+// workgroup (HalfSplit): each window takes its slots from one Map::run.
+template <int Lanes, typename Map, typename T>
+__device__ __forceinline__ void store_windows(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int x0, int n,
+                                              int tid) {
+  const HalfSplit sp = half_split(dst, n);
+  for (int g = tid; g < sp.windows; g += Lanes) {
+    const int e0 = sp.head + 8 * g;
+    const SlotRun r = Map::run(x0 + e0);
+    u16x8 v;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const T x = val(e0 + k);
-        v[k] = __builtin_bit_cast(unsigned short, x);
-      }
-      *reinterpret_cast<u16x8*>(dst + e0) = v;
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (e0 + k >= 0 && e0 + k < n) dst[e0 + k] = val(e0 + k);
+    for (int k = 0; k < 8; ++k) {
+      const T x = narrow<T>(src[run_slot<Map>(r, k)]);
+      v[k] = __builtin_bit_cast(unsigned short, x);
     }
+    *reinterpret_cast<u16x8*>(dst + e0) = v;
+  }
+  if (tid < sp.head) dst[tid] = narrow<T>(src[Map::slot(x0 + tid)]);
+  if (tid < sp.tail) {
+    const int e = n - sp.tail + tid;
+    dst[e] = narrow<T>(src[Map::slot(x0 + e)]);
   }
 }
 
@@ -117,8 +166,8 @@ template <typename Lay, typename V, typename S> __device__ __forceinline__ V lds
 
 // One thread's share of NR rows moved into LDS, in two phases: fetch() issues the thread's
 // global loads of src[r][first, first + n) into registers; commit() writes them to
-// dst[r][slot(first + e)] and returns whether any element of a row in RangeRows (bit r for
-// row r) lies beyond the polynomial range of sin_cos_wide.  MaxN bounds n at compile time.
+// dst[r][Map::slot(first + e)] and returns whether any element of a row in RangeRows (bit r
+// for row r) lies beyond the polynomial range of sin_cos_wide.  MaxN bounds n at compile time.
 // A 16-byte group never straddles a lane segment, so its elements land in consecutive slots;
 // Vec writes it with one vector LDS store (slots 16-byte aligned), otherwise element by
 // element.
@@ -149,8 +198,8 @@ template <int NR, int MaxN, int Lanes, typename T, bool Half = sizeof(T) == 2> s
     }
   }
 
-  template <bool Vec, unsigned RangeRows, typename SlotFn>
-  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid, SlotFn slot) const {
+  template <bool Vec, unsigned RangeRows, typename Map>
+  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid) const {
     bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -158,7 +207,7 @@ template <int NR, int MaxN, int Lanes, typename T, bool Half = sizeof(T) == 2> s
       if (g < groups) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          R* const d = dst[r] + slot(first + E * g);
+          R* const d = dst[r] + Map::slot(first + E * g);
           if constexpr (Vec) {
             *reinterpret_cast<typename Unit<T>::Local*>(d) = buf[r][j];
           } else {
@@ -175,7 +224,7 @@ template <int NR, int MaxN, int Lanes, typename T, bool Half = sizeof(T) == 2> s
     if (te < n) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        dst[r][slot(first + te)] = tail[r];
+        dst[r][Map::slot(first + te)] = tail[r];
         if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(tail[r]);
       }
     }
@@ -186,48 +235,63 @@ template <int NR, int MaxN, int Lanes, typename T, bool Half = sizeof(T) == 2> s
 // float16/bfloat16 rows move in 16-byte windows (above).
 template <int NR, int MaxN, int Lanes, typename T> struct RowFetch<NR, MaxN, Lanes, T, true> {
   using R = compute_t<T>;
-  static constexpr int kPer = (MaxN / 8 + 1 + Lanes - 1) / Lanes;  // a misaligned row spans one more window
+  static constexpr int kPer = (MaxN / 8 + Lanes - 1) / Lanes;
   u16x8 buf[NR][kPer];
-  int first, n, lead[NR], windows[NR];
+  T head_v[NR], tail_v[NR];  // this thread's element of the head and of the tail, if any
+  HalfSplit sp[NR];
+  int first, n;
 
   __device__ __forceinline__ void fetch(const T* const (&src)[NR], int first_, int n_, int tid) {
     first = first_;
     n = n_;
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      lead[r] = window_lead(src[r] + first);
-      windows[r] = window_count<T>(n, lead[r]);
-    }
+    for (int r = 0; r < NR; ++r) sp[r] = half_split(src[r] + first, n);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int g = tid + j * Lanes;
 #pragma unroll
       for (int r = 0; r < NR; ++r)
-        if (g < windows[r]) buf[r][j] = *reinterpret_cast<const u16x8*>(src[r] + first - lead[r] + 8 * g);
+        if (g < sp[r].windows) buf[r][j] = *reinterpret_cast<const u16x8*>(src[r] + first + sp[r].head + 8 * g);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (tid < sp[r].head) head_v[r] = src[r][first + tid];
+      if (tid < sp[r].tail) tail_v[r] = src[r][first + n - sp[r].tail + tid];
     }
   }
 
-  template <bool Vec, unsigned RangeRows, typename SlotFn>
-  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid, SlotFn slot) const {
+  template <bool Vec, unsigned RangeRows, typename Map>
+  __device__ __forceinline__ bool commit(R* const (&dst)[NR], int tid) const {
     bool wide = false;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int g = tid + j * Lanes;
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        if (g < windows[r]) {
+        if (g < sp[r].windows) {
+          const SlotRun run = Map::run(first + sp[r].head + 8 * g);
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            const int e = 8 * g - lead[r] + k;
-            if (e >= 0 && e < n) {
-              // Through a scalar: a bit cast of the vector element itself reads element 0.
-              const unsigned short bits = buf[r][j][k];
-              const R v = widen(__builtin_bit_cast(T, bits));
-              dst[r][slot(first + e)] = v;
-              if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(v);
-            }
+            // Through a scalar: a bit cast of the vector element itself reads element 0.
+            const unsigned short bits = buf[r][j][k];
+            const R v = widen(__builtin_bit_cast(T, bits));
+            dst[r][run_slot<Map>(run, k)] = v;
+            if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(v);
           }
         }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (tid < sp[r].head) {
+        const R v = widen(head_v[r]);
+        dst[r][Map::slot(first + tid)] = v;
+        if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(v);
+      }
+      if (tid < sp[r].tail) {
+        const R v = widen(tail_v[r]);
+        dst[r][Map::slot(first + n - sp[r].tail + tid)] = v;
+        if ((RangeRows >> r) & 1u) wide = wide || beyond_wide_reduce(v);
       }
     }
     return wide;
@@ -239,19 +303,18 @@ template <int NR, int MaxN, int Lanes, typename T> struct RowFetch<NR, MaxN, Lan
 // workgroup pays one memory latency per staging phase, not one per group.  Returns whether
 // any element this thread staged from a row in RangeRows lies beyond the polynomial range of
 // sin_cos_wide (RowFetch).
-template <int NR, int MaxN, int Lanes, bool Vec, unsigned RangeRows = 0, typename T, typename SlotFn>
+template <int NR, int MaxN, int Lanes, bool Vec, typename Map, unsigned RangeRows = 0, typename T>
 __device__ __forceinline__ bool stage_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int first, int n,
-                                           int tid, SlotFn slot) {
+                                           int tid) {
   RowFetch<NR, MaxN, Lanes, T> rows;
   rows.fetch(src, first, n, tid);
-  return rows.template commit<Vec, RangeRows>(dst, tid, slot);
+  return rows.template commit<Vec, RangeRows, Map>(dst, tid);
 }
 
 // NR step rows (n <= kCap elements each) into step layouts; see stage_rows for RangeRows.
 template <typename Lay, int NR, unsigned RangeRows = 0, typename T>
 __device__ __forceinline__ bool load_step_rows(compute_t<T>* const (&dst)[NR], const T* const (&src)[NR], int n, int tid) {
-  return stage_rows<NR, Lay::kCap, Lay::kLanes, Lay::kVec, RangeRows, T>(dst, src, 0, n, tid,
-                                                                         [](int s) { return Lay::step_slot(s); });
+  return stage_rows<NR, Lay::kCap, Lay::kLanes, Lay::kVec, StepRowMap<Lay>, RangeRows, T>(dst, src, 0, n, tid);
 }
 
 // NR (points, 3) rows into point layouts.
@@ -262,8 +325,7 @@ __device__ __forceinline__ void load_point_rows(compute_t<T>* const (&dst)[NR], 
 #pragma unroll
     for (int r = 0; r < NR; ++r) dst[r][tid] = widen(src[r][tid]);
   }
-  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, 0u, T>(dst, src, 9, 3 * points - 9, tid,
-                                                           [](int e) { return Lay::point_slot(e); });
+  stage_rows<NR, 3 * Lay::kCap, Lay::kLanes, Lay::kVec, PointRowMap<Lay>, 0u, T>(dst, src, 9, 3 * points - 9, tid);
 }
 
 // Two (points, 3) rows of different element types (float positions, the gradients of a
@@ -276,7 +338,6 @@ __device__ __forceinline__ void load_point_rows_pair(compute_t<TA>* da, const TA
     da[tid] = widen(sa[tid]);
     db[tid] = widen(sb[tid]);
   }
-  auto slot = [](int e) { return Lay::point_slot(e); };
   const TA* const src_a[1] = {sa};
   const TB* const src_b[1] = {sb};
   compute_t<TA>* const dst_a[1] = {da};
@@ -285,8 +346,8 @@ __device__ __forceinline__ void load_point_rows_pair(compute_t<TA>* da, const TA
   RowFetch<1, 3 * Lay::kCap, Lay::kLanes, TB> b;
   a.fetch(src_a, 9, 3 * points - 9, tid);
   b.fetch(src_b, 9, 3 * points - 9, tid);
-  a.template commit<Lay::kVec, 0u>(dst_a, tid, slot);
-  b.template commit<Lay::kVec, 0u>(dst_b, tid, slot);
+  a.template commit<Lay::kVec, 0u, PointRowMap<Lay>>(dst_a, tid);
+  b.template commit<Lay::kVec, 0u, PointRowMap<Lay>>(dst_b, tid);
 }
 
 // One lane's run of n <= N consecutive elements between global memory and registers, in
@@ -373,7 +434,7 @@ __device__ __forceinline__ void store_point_row(T* __restrict__ dst, const compu
       *reinterpret_cast<f64x2u*>(dst + 9 + 2 * g) = lds_vec<Lay, f64x2>(src + Lay::point_slot(9 + 2 * g));
     if ((n & 1) && tid == 0) dst[9 + n - 1] = src[Lay::point_slot(9 + n - 1)];
   } else {
-    store_windows<Lay::kLanes>(dst + 9, n, tid, [&](int e) { return narrow<T>(src[Lay::point_slot(9 + e)]); });
+    store_windows<Lay::kLanes, PointRowMap<Lay>>(dst + 9, src, 9, n, tid);
   }
 }
 
@@ -402,9 +463,9 @@ __device__ __forceinline__ void store_interleaved_rows(T* __restrict__ a, T* __r
       c[s] = p[2];
     }
   } else if constexpr (sizeof(T) == 2) {
-    store_windows<Lay::kLanes>(a, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s)]); });
-    store_windows<Lay::kLanes>(b, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s) + 1]); });
-    store_windows<Lay::kLanes>(c, steps, tid, [&](int s) { return narrow<T>(src[Lay::point_slot(9 + 3 * s) + 2]); });
+    store_windows<Lay::kLanes, StepPointMap<Lay>>(a, src, 0, steps, tid);
+    store_windows<Lay::kLanes, StepPointMap<Lay>>(b, src + 1, 0, steps, tid);
+    store_windows<Lay::kLanes, StepPointMap<Lay>>(c, src + 2, 0, steps, tid);
   } else {
     for (int s = tid; s < steps; s += Lay::kLanes) {
       const compute_t<T>* p = src + Lay::point_slot(9 + 3 * s);
