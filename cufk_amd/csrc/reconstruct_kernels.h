@@ -25,7 +25,8 @@ namespace cufk_amd {
 // When the position-based adjoint is accurate: every bond length positive, every bond angle
 // with sin >= kSinMin, and every coordinate within kScale shortest bonds of the origin (the
 // stored positions then resolve bond directions to about kScale ulp / bond).  float16/bfloat16
-// positions are too coarse, so those chains always take the exact path.
+// outputs are too coarse for it; their float copy (reconstruct_forward_shadow_kernel) takes
+// the float test.
 template <typename T> struct FastPath {
   static constexpr bool kEnabled = false;
   static constexpr double kSinMin = 2.0;
