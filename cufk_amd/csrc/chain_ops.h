@@ -620,6 +620,22 @@ template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up(const Ri
   return y;
 }
 
+// x of lane - 1 through the wave_shr:1 DPP move; lane 0, which has no source, keeps `fill`.
+__device__ __forceinline__ float wave_shr1(float x, float fill) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill),
+                                                               __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
+}
+
+// Float rigids move with DPP, without the LDS round trips of __shfl_up.
+__device__ __forceinline__ Rigid<float> wave_shift_up(const Rigid<float>& x, int) {
+  Rigid<float> y;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) y.m[i] = wave_shr1(x.m[i], (i % 4 == 0) ? 1.0f : 0.0f);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) y.v[i] = wave_shr1(x.v[i], 0.0f);
+  return y;
+}
+
 // Additive force/moment pair (torsion.cu:184-211).
 template <typename R> struct ForceMoment {
   V3<R> f, m;
@@ -655,6 +671,34 @@ template <typename R> __device__ __forceinline__ R wave_max(R x) {
   for (int d = 32; d >= 1; d >>= 1) x = fmax(x, __shfl_xor(x, d));
   return x;
 }
+
+// Wave-wide op-reduction of 32-bit integers through the DPP row shifts and broadcasts of the
+// scan (lane 63 ends with the whole wave), read back to every lane.  op must be idempotent:
+// lanes with no DPP source combine their value with itself.
+template <typename Op> __device__ __forceinline__ int wave_reduce_i32(int x, Op op) {
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xf, 0xf, false));  // row_shr:1
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xf, 0xf, false));  // row_shr:2
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xf, 0xf, false));  // row_shr:4
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xf, 0xf, false));  // row_shr:8
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Wave-wide minimum of positive floats and maximum of non-negative floats for the regularity
+// test, as integer min/max of the bit patterns (positive floats order as their patterns do).
+// Other inputs give some input's pattern: a chain with a non-positive or NaN length fails the
+// test on its own, and an infinite coordinate still compares as the largest.
+__device__ __forceinline__ float wave_min_positive(float x) {
+  auto op = [](int a, int b) { return min(a, b); };
+  return __builtin_bit_cast(float, wave_reduce_i32(__builtin_bit_cast(int, x), op));
+}
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  auto op = [](int a, int b) { return max(a, b); };
+  return __builtin_bit_cast(float, wave_reduce_i32(__builtin_bit_cast(int, x), op));
+}
+__device__ __forceinline__ double wave_min_positive(double x) { return wave_min(x); }
+__device__ __forceinline__ double wave_max_nonneg(double x) { return wave_max(x); }
 
 template <typename R> __device__ __forceinline__ V3<R> load3(const R* p) { return {p[0], p[1], p[2]}; }
 

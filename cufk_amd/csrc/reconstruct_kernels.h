@@ -321,8 +321,8 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   if constexpr (Fast::kEnabled) {
     if (regular != nullptr) {
       const bool wave_ok = __all(ok);
-      const R wmin = wave_min(lmin);
-      const R wmax = wave_max(xmax);
+      const R wmin = wave_min_positive(lmin);
+      const R wmax = wave_max_nonneg(xmax);
       if (lane == 0) {
         wave_stat[wave][0] = wave_ok ? R(1) : R(0);
         wave_stat[wave][1] = wmin;
@@ -773,8 +773,8 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
   }
   {
     const bool wave_ok = __all(ok);
-    const R wmin = wave_min(lmin);
-    const R wmax = wave_max(xmax);
+    const R wmin = wave_min_positive(lmin);
+    const R wmax = wave_max_nonneg(xmax);
     if (lane == 0) {
       wave_stat[wave][0] = wave_ok ? R(1) : R(0);
       wave_stat[wave][1] = wmin;
