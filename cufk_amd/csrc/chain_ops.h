@@ -713,6 +713,41 @@ template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(
   return b;
 }
 
+// Float force/moment sums cross lanes with DPP instead of the LDS round trips of the shuffles
+// above.  Inclusive suffix sum of x over the wave: row_shl adds within each row of 16 lanes,
+// after which each row's first lane holds the row's total; the totals of the later rows are
+// read back and added.
+template <int Ctrl> __device__ __forceinline__ float dpp_or_zero(float v) {  // 0 where the lane has no source
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_suffix_sum(float x, int lane) {
+  x += dpp_or_zero<0x101>(x);  // row_shl:1, lane + 1 in the same row
+  x += dpp_or_zero<0x102>(x);  // row_shl:2
+  x += dpp_or_zero<0x104>(x);  // row_shl:4
+  x += dpp_or_zero<0x108>(x);  // row_shl:8
+  auto lane_value = [](float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  };
+  const float r3 = lane_value(x, 48);
+  const float r2 = lane_value(x, 32) + r3;
+  const float r1 = lane_value(x, 16) + r2;
+  const int row = lane >> 4;
+  return x + (row == 0 ? r1 : row == 1 ? r2 : row == 2 ? r3 : 0.0f);
+}
+__device__ __forceinline__ ForceMoment<float> wave_suffix(ForceMoment<float> a, int lane) {
+  a.f = {wave_suffix_sum(a.f.x, lane), wave_suffix_sum(a.f.y, lane), wave_suffix_sum(a.f.z, lane)};
+  a.m = {wave_suffix_sum(a.m.x, lane), wave_suffix_sum(a.m.y, lane), wave_suffix_sum(a.m.z, lane)};
+  return a;
+}
+// x of lane + 1 through the wave_shl:1 DPP move; lane 63, which has no source, gets 0.
+__device__ __forceinline__ ForceMoment<float> wave_shift_down(const ForceMoment<float>& a, int) {
+  constexpr int kShl1 = 0x130;
+  ForceMoment<float> b;
+  b.f = {dpp_or_zero<kShl1>(a.f.x), dpp_or_zero<kShl1>(a.f.y), dpp_or_zero<kShl1>(a.f.z)};
+  b.m = {dpp_or_zero<kShl1>(a.m.x), dpp_or_zero<kShl1>(a.m.y), dpp_or_zero<kShl1>(a.m.z)};
+  return b;
+}
+
 // ------------------------------------------------------------------ workgroup scans
 
 template <typename R, int W>
