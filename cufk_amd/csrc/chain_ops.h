@@ -493,6 +493,21 @@ __device__ __forceinline__ double dpp_move(double old, double src) {
   return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
 }
 
+// x of lane ^ D (D < 32) through ds_swizzle's bit mode (and-mask 0x1f, xor-mask D): no
+// address register, unlike __shfl_xor's ds_bpermute.
+template <int D> __device__ __forceinline__ int lane_xor(int x) {
+  static_assert(D > 0 && D < 32, "swizzle masks reach within 32 lanes");
+  return __builtin_amdgcn_ds_swizzle(x, 0x1f | (D << 10));
+}
+template <int D> __device__ __forceinline__ float lane_xor(float x) {
+  return __builtin_bit_cast(float, lane_xor<D>(__builtin_bit_cast(int, x)));
+}
+template <int D> __device__ __forceinline__ double lane_xor(double x) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const int lo = lane_xor<D>(static_cast<int>(u)), hi = lane_xor<D>(static_cast<int>(u >> 32));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
 template <int Ctrl, int RowMask, typename R>
 __device__ __forceinline__ Rigid<R> dpp_rigid(const Rigid<R>& x) {
   Rigid<R> y;

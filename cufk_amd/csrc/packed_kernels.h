@@ -47,58 +47,71 @@ template <int G, typename R> __device__ __forceinline__ Rigid<R> group_exclusive
     if constexpr (G >= 4) x = group_scan_round<kRowShr2, 2, G>(x, t);
     if constexpr (G >= 8) x = group_scan_round<kRowShr4, 4, G>(x, t);
     if constexpr (G >= 16) x = group_scan_round<kRowShr8, 8, G>(x, t);
+    // Shift by one lane inside the row (row_shr:1); a group's first lane takes the identity.
     Rigid<R> y;
 #pragma unroll
     for (int i = 0; i < 9; ++i) {
-      const R v = __shfl_up(x.m[i], 1);
-      y.m[i] = t == 0 ? ((i % 4 == 0) ? R(1) : R(0)) : v;
+      const R id = (i % 4 == 0) ? R(1) : R(0);
+      const R v = dpp_move<kRowShr1, 0xf>(id, x.m[i]);
+      y.m[i] = t == 0 ? id : v;
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      const R v = __shfl_up(x.v[i], 1);
+      const R v = dpp_move<kRowShr1, 0xf>(R(0), x.v[i]);
       y.v[i] = t == 0 ? R(0) : v;
     }
     return y;
   }
 }
 
+// x of lane + D inside the group (row_shl:D; groups lie inside one DPP row), else 0.
+template <int D, int G, typename R> __device__ __forceinline__ R group_down(R x, int t) {
+  const R y = dpp_move<0x100 + D, 0xf>(R(0), x);
+  return t + D < G ? y : R(0);
+}
+
 // Exclusive suffix sum over each group (zero in the group's last lane).
 template <int G, typename R> __device__ __forceinline__ ForceMoment<R> group_suffix(ForceMoment<R> a, int lane) {
   const int t = lane & (G - 1);
-  auto down = [&](R x, int d) {
-    const R y = __shfl_down(x, d);
-    return t + d < G ? y : R(0);
+  auto round = [&]<int D>() {
+    if constexpr (D < G) {
+      a.f = {a.f.x + group_down<D, G>(a.f.x, t), a.f.y + group_down<D, G>(a.f.y, t), a.f.z + group_down<D, G>(a.f.z, t)};
+      a.m = {a.m.x + group_down<D, G>(a.m.x, t), a.m.y + group_down<D, G>(a.m.y, t), a.m.z + group_down<D, G>(a.m.z, t)};
+    }
   };
-#pragma unroll
-  for (int d = 1; d < G; d <<= 1) {
-    a.f.x += down(a.f.x, d);
-    a.f.y += down(a.f.y, d);
-    a.f.z += down(a.f.z, d);
-    a.m.x += down(a.m.x, d);
-    a.m.y += down(a.m.y, d);
-    a.m.z += down(a.m.z, d);
-  }
+  round.template operator()<1>();
+  round.template operator()<2>();
+  round.template operator()<4>();
+  round.template operator()<8>();
   ForceMoment<R> e;
-  e.f = {down(a.f.x, 1), down(a.f.y, 1), down(a.f.z, 1)};
-  e.m = {down(a.m.x, 1), down(a.m.y, 1), down(a.m.z, 1)};
+  if constexpr (G == 1) {
+    e = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
+  } else {
+    e.f = {group_down<1, G>(a.f.x, t), group_down<1, G>(a.f.y, t), group_down<1, G>(a.f.z, t)};
+    e.m = {group_down<1, G>(a.m.x, t), group_down<1, G>(a.m.y, t), group_down<1, G>(a.m.z, t)};
+  }
   return e;
 }
 
+// Reductions over each group of G lanes (aligned, G <= 16) by swizzled exchanges.
+template <int G, typename V, typename Op> __device__ __forceinline__ V group_reduce(V x, Op op) {
+  auto round = [&]<int D>() {
+    if constexpr (D < G) x = op(x, lane_xor<D>(x));
+  };
+  round.template operator()<1>();
+  round.template operator()<2>();
+  round.template operator()<4>();
+  round.template operator()<8>();
+  return x;
+}
 template <int G> __device__ __forceinline__ bool group_all(bool p) {
-  int v = p ? 1 : 0;
-#pragma unroll
-  for (int d = 1; d < G; d <<= 1) v &= __shfl_xor(v, d);
-  return v != 0;
+  return group_reduce<G>(p ? 1 : 0, [](int a, int b) { return a & b; }) != 0;
 }
 template <int G, typename R> __device__ __forceinline__ R group_min(R x) {
-#pragma unroll
-  for (int d = 1; d < G; d <<= 1) x = fmin(x, __shfl_xor(x, d));
-  return x;
+  return group_reduce<G>(x, [](R a, R b) { return fmin(a, b); });
 }
 template <int G, typename R> __device__ __forceinline__ R group_max(R x) {
-#pragma unroll
-  for (int d = 1; d < G; d <<= 1) x = fmax(x, __shfl_xor(x, d));
-  return x;
+  return group_reduce<G>(x, [](R a, R b) { return fmax(a, b); });
 }
 
 // ---------------------------------------------------------------------------- flat staging
