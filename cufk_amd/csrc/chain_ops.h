@@ -13,6 +13,7 @@
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
+#include <limits>
 
 namespace cufk_amd {
 
@@ -485,6 +486,9 @@ __device__ __forceinline__ float dpp_move(float old, float src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
                                                                Ctrl, RowMask, 0xf, false));
 }
+template <int Ctrl, int RowMask> __device__ __forceinline__ int dpp_move(int old, int src) {
+  return __builtin_amdgcn_update_dpp(old, src, Ctrl, RowMask, 0xf, false);
+}
 template <int Ctrl, int RowMask>
 __device__ __forceinline__ double dpp_move(double old, double src) {
   const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, src);
@@ -619,35 +623,32 @@ template <int W> __device__ __forceinline__ bool block_any(bool v, int (&flags)[
   return any;
 }
 
-// Value of lane-1 (identity in lane 0).
-template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up(const Rigid<R>& x, int lane) {
+// ------------------------------------------------------------------ lane exchanges
+// Every exchange across lanes is a DPP move (or a v_readlane): __shfl_* compiles to
+// ds_bpermute plus VALU instructions for the lane address, and waits on an LDS round trip.
+
+constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
+constexpr int kWaveShl1 = 0x130, kWaveShr1 = 0x138;
+
+// v of lane l, in every lane.
+__device__ __forceinline__ int lane_value(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double lane_value(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(u), l);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), l);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
+// Value of lane-1 (identity in lane 0), by the wave_shr:1 DPP move.
+template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up(const Rigid<R>& x, int) {
   Rigid<R> y;
 #pragma unroll
-  for (int i = 0; i < 9; ++i) {
-    const R t = __shfl_up(x.m[i], 1);
-    y.m[i] = lane == 0 ? ((i % 4 == 0) ? R(1) : R(0)) : t;
-  }
+  for (int i = 0; i < 9; ++i) y.m[i] = dpp_move<kWaveShr1, 0xf>((i % 4 == 0) ? R(1) : R(0), x.m[i]);
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const R t = __shfl_up(x.v[i], 1);
-    y.v[i] = lane == 0 ? R(0) : t;
-  }
-  return y;
-}
-
-// x of lane - 1 through the wave_shr:1 DPP move; lane 0, which has no source, keeps `fill`.
-__device__ __forceinline__ float wave_shr1(float x, float fill) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill),
-                                                               __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
-}
-
-// Float rigids move with DPP, without the LDS round trips of __shfl_up.
-__device__ __forceinline__ Rigid<float> wave_shift_up(const Rigid<float>& x, int) {
-  Rigid<float> y;
-#pragma unroll
-  for (int i = 0; i < 9; ++i) y.m[i] = wave_shr1(x.m[i], (i % 4 == 0) ? 1.0f : 0.0f);
-#pragma unroll
-  for (int i = 0; i < 3; ++i) y.v[i] = wave_shr1(x.v[i], 0.0f);
+  for (int i = 0; i < 3; ++i) y.v[i] = dpp_move<kWaveShr1, 0xf>(R(0), x.v[i]);
   return y;
 }
 
@@ -656,112 +657,73 @@ template <typename R> struct ForceMoment {
   V3<R> f, m;
 };
 
-template <typename R> __device__ __forceinline__ R shfl_down_or_zero(R x, int d, int lane) {
-  const R t = __shfl_down(x, d);
-  return lane + d < 64 ? t : R(0);
-}
-
-// Inclusive right-to-left (suffix) sum over the lanes of a wave.
-template <typename R> __device__ __forceinline__ ForceMoment<R> wave_suffix(ForceMoment<R> a, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    a.f.x += shfl_down_or_zero(a.f.x, d, lane);
-    a.f.y += shfl_down_or_zero(a.f.y, d, lane);
-    a.f.z += shfl_down_or_zero(a.f.z, d, lane);
-    a.m.x += shfl_down_or_zero(a.m.x, d, lane);
-    a.m.y += shfl_down_or_zero(a.m.y, d, lane);
-    a.m.z += shfl_down_or_zero(a.m.z, d, lane);
-  }
-  return a;
-}
-
-template <typename R> __device__ __forceinline__ R wave_min(R x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x = fmin(x, __shfl_xor(x, d));
-  return x;
-}
-
-template <typename R> __device__ __forceinline__ R wave_max(R x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x = fmax(x, __shfl_xor(x, d));
-  return x;
-}
-
-// Wave-wide op-reduction of 32-bit integers through the DPP row shifts and broadcasts of the
-// scan (lane 63 ends with the whole wave), read back to every lane.  op must be idempotent:
-// lanes with no DPP source combine their value with itself.
-template <typename Op> __device__ __forceinline__ int wave_reduce_i32(int x, Op op) {
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xf, 0xf, false));  // row_shr:1
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xf, 0xf, false));  // row_shr:2
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xf, 0xf, false));  // row_shr:4
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xf, 0xf, false));  // row_shr:8
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
-  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
-  return __builtin_amdgcn_readlane(x, 63);
-}
-
-// Wave-wide minimum of positive floats and maximum of non-negative floats for the regularity
-// test, as integer min/max of the bit patterns (positive floats order as their patterns do).
-// Other inputs give some input's pattern: a chain with a non-positive or NaN length fails the
-// test on its own, and an infinite coordinate still compares as the largest.
-__device__ __forceinline__ float wave_min_positive(float x) {
-  auto op = [](int a, int b) { return min(a, b); };
-  return __builtin_bit_cast(float, wave_reduce_i32(__builtin_bit_cast(int, x), op));
-}
-__device__ __forceinline__ float wave_max_nonneg(float x) {
-  auto op = [](int a, int b) { return max(a, b); };
-  return __builtin_bit_cast(float, wave_reduce_i32(__builtin_bit_cast(int, x), op));
-}
-__device__ __forceinline__ double wave_min_positive(double x) { return wave_min(x); }
-__device__ __forceinline__ double wave_max_nonneg(double x) { return wave_max(x); }
-
-template <typename R> __device__ __forceinline__ V3<R> load3(const R* p) { return {p[0], p[1], p[2]}; }
-
-template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(const ForceMoment<R>& a, int lane) {
-  ForceMoment<R> b;
-  b.f.x = shfl_down_or_zero(a.f.x, 1, lane);
-  b.f.y = shfl_down_or_zero(a.f.y, 1, lane);
-  b.f.z = shfl_down_or_zero(a.f.z, 1, lane);
-  b.m.x = shfl_down_or_zero(a.m.x, 1, lane);
-  b.m.y = shfl_down_or_zero(a.m.y, 1, lane);
-  b.m.z = shfl_down_or_zero(a.m.z, 1, lane);
-  return b;
-}
-
-// Float force/moment sums cross lanes with DPP instead of the LDS round trips of the shuffles
-// above.  Inclusive suffix sum of x over the wave: row_shl adds within each row of 16 lanes,
-// after which each row's first lane holds the row's total; the totals of the later rows are
-// read back and added.
-template <int Ctrl> __device__ __forceinline__ float dpp_or_zero(float v) {  // 0 where the lane has no source
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float wave_suffix_sum(float x, int lane) {
-  x += dpp_or_zero<0x101>(x);  // row_shl:1, lane + 1 in the same row
-  x += dpp_or_zero<0x102>(x);  // row_shl:2
-  x += dpp_or_zero<0x104>(x);  // row_shl:4
-  x += dpp_or_zero<0x108>(x);  // row_shl:8
-  auto lane_value = [](float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-  };
-  const float r3 = lane_value(x, 48);
-  const float r2 = lane_value(x, 32) + r3;
-  const float r1 = lane_value(x, 16) + r2;
+// Inclusive right-to-left (suffix) sum over the lanes of a wave: row_shl adds within each row
+// of 16 lanes, after which each row's first lane holds the row's total; the totals of the
+// later rows are read back and added.
+template <typename R> __device__ __forceinline__ R wave_suffix_sum(R x, int lane) {
+  x += dpp_move<kRowShl1, 0xf>(R(0), x);  // lane + 1 in the same row, else 0
+  x += dpp_move<kRowShl2, 0xf>(R(0), x);
+  x += dpp_move<kRowShl4, 0xf>(R(0), x);
+  x += dpp_move<kRowShl8, 0xf>(R(0), x);
+  const R r3 = lane_value(x, 48);
+  const R r2 = lane_value(x, 32) + r3;
+  const R r1 = lane_value(x, 16) + r2;
   const int row = lane >> 4;
-  return x + (row == 0 ? r1 : row == 1 ? r2 : row == 2 ? r3 : 0.0f);
+  return x + (row == 0 ? r1 : row == 1 ? r2 : row == 2 ? r3 : R(0));
 }
-__device__ __forceinline__ ForceMoment<float> wave_suffix(ForceMoment<float> a, int lane) {
+template <typename R> __device__ __forceinline__ ForceMoment<R> wave_suffix(ForceMoment<R> a, int lane) {
   a.f = {wave_suffix_sum(a.f.x, lane), wave_suffix_sum(a.f.y, lane), wave_suffix_sum(a.f.z, lane)};
   a.m = {wave_suffix_sum(a.m.x, lane), wave_suffix_sum(a.m.y, lane), wave_suffix_sum(a.m.z, lane)};
   return a;
 }
-// x of lane + 1 through the wave_shl:1 DPP move; lane 63, which has no source, gets 0.
-__device__ __forceinline__ ForceMoment<float> wave_shift_down(const ForceMoment<float>& a, int) {
-  constexpr int kShl1 = 0x130;
-  ForceMoment<float> b;
-  b.f = {dpp_or_zero<kShl1>(a.f.x), dpp_or_zero<kShl1>(a.f.y), dpp_or_zero<kShl1>(a.f.z)};
-  b.m = {dpp_or_zero<kShl1>(a.m.x), dpp_or_zero<kShl1>(a.m.y), dpp_or_zero<kShl1>(a.m.z)};
+
+// Value of lane+1 (zero in lane 63), by the wave_shl:1 DPP move.
+template <typename R> __device__ __forceinline__ ForceMoment<R> wave_shift_down(const ForceMoment<R>& a, int) {
+  ForceMoment<R> b;
+  b.f = {dpp_move<kWaveShl1, 0xf>(R(0), a.f.x), dpp_move<kWaveShl1, 0xf>(R(0), a.f.y),
+         dpp_move<kWaveShl1, 0xf>(R(0), a.f.z)};
+  b.m = {dpp_move<kWaveShl1, 0xf>(R(0), a.m.x), dpp_move<kWaveShl1, 0xf>(R(0), a.m.y),
+         dpp_move<kWaveShl1, 0xf>(R(0), a.m.z)};
   return b;
 }
+
+// Wave-wide reduction along the scan's DPP pattern (row shifts, then the two row
+// broadcasts; lane 63 ends with the whole wave), read back to every lane.  Lanes with no DPP
+// source receive `none`: the identity of op.
+template <typename V, typename Op> __device__ __forceinline__ V wave_reduce(V x, V none, Op op) {
+  x = op(x, dpp_move<kRowShr1, 0xf>(none, x));
+  x = op(x, dpp_move<kRowShr2, 0xf>(none, x));
+  x = op(x, dpp_move<kRowShr4, 0xf>(none, x));
+  x = op(x, dpp_move<kRowShr8, 0xf>(none, x));
+  x = op(x, dpp_move<kRowBcast15, 0xa>(none, x));
+  x = op(x, dpp_move<kRowBcast31, 0xc>(none, x));
+  return lane_value(x, 63);
+}
+template <typename R> __device__ __forceinline__ R wave_sum(R x) {
+  return wave_reduce(x, R(0), [](R a, R b) { return a + b; });
+}
+
+// Wave-wide minimum of positive values and maximum of non-negative values for the regularity
+// test.  Floats reduce as integer min/max of their bit patterns (positive floats order as
+// their patterns do; no canonicalising of NaNs as fmin/fmax need).  Other inputs give some
+// input's pattern: a chain with a non-positive or NaN length fails the test on its own, and an
+// infinite coordinate still compares as the largest.
+__device__ __forceinline__ float wave_min_positive(float x) {
+  const int r = wave_reduce(__builtin_bit_cast(int, x), 0x7fffffff, [](int a, int b) { return min(a, b); });
+  return __builtin_bit_cast(float, r);
+}
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  const int r = wave_reduce(__builtin_bit_cast(int, x), static_cast<int>(0x80000000u), [](int a, int b) { return max(a, b); });
+  return __builtin_bit_cast(float, r);
+}
+__device__ __forceinline__ double wave_min_positive(double x) {
+  return wave_reduce(x, std::numeric_limits<double>::infinity(), [](double a, double b) { return fmin(a, b); });
+}
+__device__ __forceinline__ double wave_max_nonneg(double x) {
+  return wave_reduce(x, 0.0, [](double a, double b) { return fmax(a, b); });
+}
+
+template <typename R> __device__ __forceinline__ V3<R> load3(const R* p) { return {p[0], p[1], p[2]}; }
 
 // ------------------------------------------------------------------ workgroup scans
 

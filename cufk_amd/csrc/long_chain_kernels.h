@@ -111,9 +111,9 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
     }
     Rigid<double> chunk;
 #pragma unroll
-    for (int i = 0; i < 9; ++i) chunk.m[i] = __shfl(incl.m[i], 63);
+    for (int i = 0; i < 9; ++i) chunk.m[i] = lane_value(incl.m[i], 63);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) chunk.v[i] = __shfl(incl.v[i], 63);
+    for (int i = 0; i < 3; ++i) chunk.v[i] = lane_value(incl.v[i], 63);
     run = compose(run, chunk);
   }
 }
@@ -142,12 +142,6 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_place_kernel(T* __r
 }
 
 // ---------------------------------------------------------------------------- backward
-
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
-}
 
 // Segments j >= 1: F and M about the segment's x2 over its own points, from the saved
 // positions, in double.
@@ -183,7 +177,7 @@ __global__ __launch_bounds__(kLongThreads) void long_backward_sums_kernel(const 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int k = 0; k < 6; ++k) {
-    const double v = wave_sum_f64(acc[k]);
+    const double v = wave_sum(acc[k]);
     if (lane == 0) part[wave][k] = v;
   }
   __syncthreads();
@@ -222,19 +216,17 @@ static __global__ __launch_bounds__(kLongThreads) void long_backward_carry_kerne
       }
     }
     const ForceMoment<double> incl = wave_suffix(own, lane);
-    ForceMoment<double> after;  // lanes above this one, then the later chunks
-    after.f = V3<double>{shfl_down_or_zero(incl.f.x, 1, lane), shfl_down_or_zero(incl.f.y, 1, lane),
-                         shfl_down_or_zero(incl.f.z, 1, lane)} + later.f;
-    after.m = V3<double>{shfl_down_or_zero(incl.m.x, 1, lane), shfl_down_or_zero(incl.m.y, 1, lane),
-                         shfl_down_or_zero(incl.m.z, 1, lane)} + later.m;
+    ForceMoment<double> after = wave_shift_down(incl, lane);  // lanes above this one
+    after.f = after.f + later.f;                                  // then the later chunks
+    after.m = after.m + later.m;
     if (j < segments) {
       double* w = wk + j * kLongWorkDoubles + 6;
       const V3<double> m = after.m - cross(o, after.f);
       w[0] = after.f.x; w[1] = after.f.y; w[2] = after.f.z;
       w[3] = m.x; w[4] = m.y; w[5] = m.z;
     }
-    later.f = later.f + V3<double>{__shfl(incl.f.x, 0), __shfl(incl.f.y, 0), __shfl(incl.f.z, 0)};
-    later.m = later.m + V3<double>{__shfl(incl.m.x, 0), __shfl(incl.m.y, 0), __shfl(incl.m.z, 0)};
+    later.f = later.f + V3<double>{lane_value(incl.f.x, 0), lane_value(incl.f.y, 0), lane_value(incl.f.z, 0)};
+    later.m = later.m + V3<double>{lane_value(incl.m.x, 0), lane_value(incl.m.y, 0), lane_value(incl.m.z, 0)};
   }
 }
 

@@ -349,8 +349,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   }
   if constexpr (Loss) {
     __shared__ double loss_part[W];
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d);
+    acc = wave_sum(acc);
     if (lane == 0) loss_part[wave] = acc;
     __syncthreads();
     if (tid == 0) {
@@ -900,9 +899,7 @@ __global__ __launch_bounds__(kAnchorThreads) void anchor_gradients_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int k = 0; k < 6; ++k) {
-    double v = acc[k];
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    const double v = wave_sum(acc[k]);
     if (lane == 0) red[wave][k] = v;
   }
   __syncthreads();
