@@ -120,19 +120,36 @@ template <int Gap> __device__ __forceinline__ int fslot(int e) { return e + e / 
 // LDS words for a flat range of n elements (plus `over` elements read past its end).
 constexpr int flat_words(int n, int gap, int over = 0) { return n + over + (n + over) / gap + 1; }
 
-// [src, src + total) moves in 16-byte windows aligned down from src (E = 16 / sizeof(T)
-// elements each): window g covers the elements E*g - lead .. E*g - lead + E - 1, lead being
-// src's element offset in its 16-byte block.  A load may read bytes of the first and last
-// window outside the range; they share a 16-byte block, hence a page, with bytes of the range,
-// and are discarded.  Stores write whole windows only inside the range and single elements at
-// its ends.
-template <typename T> __device__ __forceinline__ int flat_lead(const T* p) {
-  return static_cast<int>((reinterpret_cast<uintptr_t>(p) / sizeof(T)) & (16 / sizeof(T) - 1));
-}
+// [src, src + total) moves as RowSplit: whole 16-byte windows (E = 16 / sizeof(T) elements),
+// head and tail elements one per thread.  A window of E <= Gap elements crosses at most one
+// segment end, so its slots follow from one division.
 constexpr int flat_windows(int elems, int elem_bytes, int lanes) {
   const int e = 16 / elem_bytes;
   return ((elems + 2 * e - 2) / e + lanes - 1) / lanes;
 }
+// fslot<Gap>(f0 + k) for 0 <= k < E: a shift per element for a power-of-two Gap, else from one
+// division (q = f0 / Gap, f0 % Gap) per window.
+template <int Gap> struct FlatRun {
+  static constexpr bool kPow2 = (Gap & (Gap - 1)) == 0;
+  int base;  // f0 for a power-of-two Gap, else fslot(f0) = f0 + q
+  int off;   // f0 % Gap (unused for a power-of-two Gap)
+  __device__ __forceinline__ explicit FlatRun(int f0) {
+    if constexpr (kPow2) {
+      base = f0;
+      off = 0;
+    } else {
+      const int q = f0 / Gap;
+      base = f0 + q;
+      off = f0 - q * Gap;
+    }
+  }
+  __device__ __forceinline__ int slot(int k) const {
+    if constexpr (kPow2)
+      return fslot<Gap>(base + k);
+    else
+      return base + k + (off + k >= Gap ? 1 : 0);
+  }
+};
 
 // dst[fslot<Gap>(f)] = src[f] for f in [0, total).  All of a thread's loads are issued before
 // its first LDS write; MaxWin bounds the windows per thread.  Returns whether any element lies
@@ -142,32 +159,42 @@ __device__ __forceinline__ bool stage_flat(compute_t<T>* dst, const T* __restric
                                            bool range) {
   using R = compute_t<T>;
   constexpr int E = 16 / sizeof(T);
-  const int lead = flat_lead(src);
-  const int windows = total > 0 ? (total + lead + E - 1) / E : 0;
+  static_assert(E <= Gap, "a window crosses at most one segment end");
+  const RowSplit sp = block_split(src, total);
   uint4 buf[MaxWin];
 #pragma unroll
   for (int j = 0; j < MaxWin; ++j) {
     const int g = tid + j * Lanes;
-    if (g < windows) buf[j] = *reinterpret_cast<const uint4*>(src - lead + E * g);
+    if (g < sp.windows) buf[j] = *reinterpret_cast<const uint4*>(src + sp.head + E * g);
   }
+  T head_v, tail_v;
+  if (tid < sp.head) head_v = src[tid];
+  if (tid < sp.tail) tail_v = src[total - sp.tail + tid];
   bool wide = false;
 #pragma unroll
   for (int j = 0; j < MaxWin; ++j) {
     const int g = tid + j * Lanes;
-    if (g < windows) {
-      const int f0 = E * g - lead;
+    if (g < sp.windows) {
+      const FlatRun<Gap> run(sp.head + E * g);
       T v[E];
       __builtin_memcpy(v, &buf[j], 16);
 #pragma unroll
       for (int k = 0; k < E; ++k) {
-        const int f = f0 + k;
-        if (f >= 0 && f < total) {
-          const R x = widen(v[k]);
-          dst[fslot<Gap>(f)] = x;
-          if (range) wide = wide || beyond_wide_reduce(x);
-        }
+        const R x = widen(v[k]);
+        dst[run.slot(k)] = x;
+        if (range) wide = wide || beyond_wide_reduce(x);
       }
     }
+  }
+  if (tid < sp.head) {
+    const R x = widen(head_v);
+    dst[fslot<Gap>(tid)] = x;
+    if (range) wide = wide || beyond_wide_reduce(x);
+  }
+  if (tid < sp.tail) {
+    const R x = widen(tail_v);
+    dst[fslot<Gap>(total - sp.tail + tid)] = x;
+    if (range) wide = wide || beyond_wide_reduce(x);
   }
   return wide;
 }
@@ -176,24 +203,22 @@ __device__ __forceinline__ bool stage_flat(compute_t<T>* dst, const T* __restric
 template <int Lanes, int Gap, typename T>
 __device__ __forceinline__ void store_flat(T* __restrict__ dst, const compute_t<T>* src, int total, int tid) {
   constexpr int E = 16 / sizeof(T);
-  const int lead = flat_lead(dst);
-  const int windows = total > 0 ? (total + lead + E - 1) / E : 0;
-  for (int g = tid; g < windows; g += Lanes) {
-    const int f0 = E * g - lead;
-    if (f0 >= 0 && f0 + E <= total) {
-      T v[E];
+  static_assert(E <= Gap, "a window crosses at most one segment end");
+  const RowSplit sp = block_split(dst, total);
+  for (int g = tid; g < sp.windows; g += Lanes) {
+    const int f0 = sp.head + E * g;
+    const FlatRun<Gap> run(f0);
+    T v[E];
 #pragma unroll
-      for (int k = 0; k < E; ++k) v[k] = narrow<T>(src[fslot<Gap>(f0 + k)]);
-      uint4 w;
-      __builtin_memcpy(&w, v, 16);
-      *reinterpret_cast<uint4*>(dst + f0) = w;
-    } else {
-#pragma unroll
-      for (int k = 0; k < E; ++k) {
-        const int f = f0 + k;
-        if (f >= 0 && f < total) dst[f] = narrow<T>(src[fslot<Gap>(f)]);
-      }
-    }
+    for (int k = 0; k < E; ++k) v[k] = narrow<T>(src[run.slot(k)]);
+    uint4 w;
+    __builtin_memcpy(&w, v, 16);
+    *reinterpret_cast<uint4*>(dst + f0) = w;
+  }
+  if (tid < sp.head) dst[tid] = narrow<T>(src[fslot<Gap>(tid)]);
+  if (tid < sp.tail) {
+    const int f = total - sp.tail + tid;
+    dst[f] = narrow<T>(src[fslot<Gap>(f)]);
   }
 }
 

@@ -108,31 +108,31 @@ template <> struct Unit<double> {
   typedef f64x2 Local;
 };
 
-// float16/bfloat16 rows are only 2-byte aligned.  A row of n elements splits at its 16-byte
-// block boundaries: `head` elements before the first boundary, `windows` whole 16-byte windows
-// of 8 elements, and `tail` elements after the last boundary (head, tail <= 7).  Windows move
-// as one 16-byte access each, head and tail elements one per thread, so no access touches
-// bytes outside the row.
+// A row of n elements that is only element-aligned splits at its 16-byte block boundaries:
+// `head` elements before the first boundary, `windows` whole 16-byte windows of 16/sizeof(T)
+// elements, and `tail` elements after the last boundary (head, tail < 16/sizeof(T)).  Windows
+// move as one 16-byte access each, head and tail elements one per thread, so no access touches
+// bytes outside the row.  float16/bfloat16 rows (2-byte aligned) always move this way.
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-struct HalfSplit {
+struct RowSplit {
   int head;
   int windows;
   int tail;
 };
-template <typename T> __device__ __forceinline__ HalfSplit half_split(const T* row, int n) {
-  static_assert(sizeof(T) == 2, "windows are for 2-byte elements");
-  const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(row) >> 1) & 7);
-  const int head = min((8 - lead) & 7, max(n, 0));
-  const int windows = (max(n, 0) - head) >> 3;
-  return {head, windows, max(n, 0) - head - 8 * windows};
+template <typename T> __device__ __forceinline__ RowSplit block_split(const T* row, int n) {
+  constexpr int E = 16 / sizeof(T);
+  const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(row) / sizeof(T)) & (E - 1));
+  const int head = min((E - lead) & (E - 1), max(n, 0));
+  const int windows = (max(n, 0) - head) / E;
+  return {head, windows, max(n, 0) - head - E * windows};
 }
 
 // dst[e] = src[Map::slot(x0 + e)] rounded to T, for e in [0, n), by the Lanes threads of a
-// workgroup (HalfSplit): each window takes its slots from one Map::run.
+// workgroup (RowSplit): each window takes its slots from one Map::run.
 template <int Lanes, typename Map, typename T>
 __device__ __forceinline__ void store_windows(T* __restrict__ dst, const compute_t<T>* __restrict__ src, int x0, int n,
                                               int tid) {
-  const HalfSplit sp = half_split(dst, n);
+  const RowSplit sp = block_split(dst, n);
   for (int g = tid; g < sp.windows; g += Lanes) {
     const int e0 = sp.head + 8 * g;
     const SlotRun r = Map::run(x0 + e0);
@@ -238,14 +238,14 @@ template <int NR, int MaxN, int Lanes, typename T> struct RowFetch<NR, MaxN, Lan
   static constexpr int kPer = (MaxN / 8 + Lanes - 1) / Lanes;
   u16x8 buf[NR][kPer];
   T head_v[NR], tail_v[NR];  // this thread's element of the head and of the tail, if any
-  HalfSplit sp[NR];
+  RowSplit sp[NR];
   int first, n;
 
   __device__ __forceinline__ void fetch(const T* const (&src)[NR], int first_, int n_, int tid) {
     first = first_;
     n = n_;
 #pragma unroll
-    for (int r = 0; r < NR; ++r) sp[r] = half_split(src[r] + first, n);
+    for (int r = 0; r < NR; ++r) sp[r] = block_split(src[r] + first, n);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int g = tid + j * Lanes;
