@@ -324,11 +324,13 @@ template <typename R> __device__ __forceinline__ V3<R> cross(V3<R> a, V3<R> b) {
 }
 
 // frame_utils.cuh:17-21: v / sqrt(max(v.v, eps)) with eps = 1e-12f.
+// v / max(|v|, 1e-6), the norm clamped as the reference clamps |v|^2 at 1e-12
+// (frame_utils.cuh:17-31), as v times one reciprocal square root instead of a square root and
+// three divisions (within 2 ulp of the quotients).
 template <typename R> __device__ __forceinline__ V3<R> normalized(V3<R> v) {
   const R n2 = dot(v, v);
   const R eps = static_cast<R>(1.0e-12f);
-  const R n = sqrt_r(n2 > eps ? n2 : eps);
-  return {v.x / n, v.y / n, v.z / n};
+  return rsqrt_r(n2 > eps ? n2 : eps) * v;
 }
 
 // ------------------------------------------------------------------ rigid transforms
