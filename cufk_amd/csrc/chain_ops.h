@@ -308,6 +308,10 @@ __device__ __forceinline__ float sqrt_r(float x) { return sqrtf(x); }
 __device__ __forceinline__ double sqrt_r(double x) { return sqrt(x); }
 __device__ __forceinline__ float rsqrt_r(float x) { return rsqrtf(x); }
 __device__ __forceinline__ double rsqrt_r(double x) { return rsqrt(x); }
+// 1/sqrt(x) for the position-based adjoint, whose regularity test keeps x normal: the bare
+// v_rsq_f32 (rsqrtf adds a rescaling for denormal x; for normal x the two agree).
+__device__ __forceinline__ float rsqrt_bond(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ double rsqrt_bond(double x) { return rsqrt(x); }
 
 // ------------------------------------------------------------------ small vectors
 

@@ -417,7 +417,7 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
         bool reg = all_ok && ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= FastPath<T>::kSinMin;
         const R mm = fmin(m, fmin(ff.L0, ff.L1));
         const R x = fmax(xm, abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2));
-        reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * mm;
+        reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * mm && mm >= static_cast<R>(FastPath<T>::kMinLength);
         regular[b0 + ln.c] = reg ? 1 : 0;
       }
     }
@@ -477,9 +477,9 @@ __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, 
       const V3<R> b1 = xa - xb;
       const V3<R> b2 = xb - xc;
       const V3<R> n = cross(b1, b2);
-      out.l[i] = dot(b1, F) * rsqrt_r(dot(b1, b1));
-      out.a[i] = dot(n, Tq) * rsqrt_r(dot(n, n));
-      out.d[i] = dot(b2, Tq) * rsqrt_r(dot(b2, b2));
+      out.l[i] = dot(b1, F) * rsqrt_bond(dot(b1, b1));
+      out.a[i] = dot(n, Tq) * rsqrt_bond(dot(n, n));
+      out.d[i] = dot(b2, Tq) * rsqrt_bond(dot(b2, b2));
     }
   }
   if (ln.leader) {  // s0 = 0: xr holds points 0, 1, 2 first
@@ -496,9 +496,9 @@ __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, 
     const V3<R> b1 = x2 - x1;
     const V3<R> b0 = x1 - x0;
     const V3<R> n = cross(b1, b0);
-    out.head[0] = dot(b0, F + g1) * rsqrt_r(dot(b0, b0));
-    out.head[1] = dot(b1, F) * rsqrt_r(dot(b1, b1));
-    out.head[2] = dot(n, Tq) * rsqrt_r(dot(n, n));
+    out.head[0] = dot(b0, F + g1) * rsqrt_bond(dot(b0, b0));
+    out.head[1] = dot(b1, F) * rsqrt_bond(dot(b1, b1));
+    out.head[2] = dot(n, Tq) * rsqrt_bond(dot(n, n));
   }
 }
 
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
       const bool reg = all_ok && ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= static_cast<R>(Fast::kSinMin);
       const R mm = fmin(m, fmin(ff.L0, ff.L1));
       const R xx = fmax(xm, abs_max3(abs_max3(R(0), a), bb));
-      irregular = !(reg && xx <= static_cast<R>(Fast::kScale) * mm);
+      irregular = !(reg && xx <= static_cast<R>(Fast::kScale) * mm && mm >= static_cast<R>(Fast::kMinLength));
     }
     positions = !block_any<W>(irregular, vote, lane, wave);  // barrier: parameter reads retired
     if (positions) {

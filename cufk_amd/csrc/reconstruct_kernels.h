@@ -24,23 +24,28 @@ namespace cufk_amd {
 
 // When the position-based adjoint is accurate: every bond length positive, every bond angle
 // with sin >= kSinMin, and every coordinate within kScale shortest bonds of the origin (the
-// stored positions then resolve bond directions to about kScale ulp / bond).  float16/bfloat16
+// stored positions then resolve bond directions to about kScale ulp / bond).  The shortest
+// bond is also at least kMinLength, which keeps every squared bond length and squared bond
+// normal that the adjoint normalises far from the denormal range (rsqrt_bond).  float16/bfloat16
 // outputs are too coarse for it; their float copy (reconstruct_forward_shadow_kernel) takes
 // the float test.
 template <typename T> struct FastPath {
   static constexpr bool kEnabled = false;
   static constexpr double kSinMin = 2.0;
   static constexpr double kScale = 0.0;
+  static constexpr double kMinLength = 0.0;
 };
 template <> struct FastPath<float> {
   static constexpr bool kEnabled = true;
   static constexpr double kSinMin = 0.5;
   static constexpr double kScale = 256.0;
+  static constexpr double kMinLength = 0x1p-20;  // |b|^2 >= 2^-40, |b1 x b2|^2 >= 2^-82
 };
 template <> struct FastPath<double> {
   static constexpr bool kEnabled = true;
   static constexpr double kSinMin = 1.0e-2;
   static constexpr double kScale = 8192.0;
+  static constexpr double kMinLength = 0.0;  // the double adjoint keeps the library rsqrt
 };
 
 template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
@@ -343,7 +348,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         m = fmin(m, wave_stat[w][1]);
         x = fmax(x, wave_stat[w][2]);
       }
-      reg = reg && x <= static_cast<R>(Fast::kScale) * m;
+      reg = reg && x <= static_cast<R>(Fast::kScale) * m && m >= static_cast<R>(Fast::kMinLength);
     }
     *regular = reg ? 1 : 0;
   }
@@ -645,9 +650,9 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
       const V3<R> b1 = xa - xb;
       const V3<R> b2 = xb - xc;
       const V3<R> n = cross(b1, b2);
-      oL[i] = dot(b1, F) * rsqrt_r(dot(b1, b1));
-      oA[i] = dot(n, Tq) * rsqrt_r(dot(n, n));
-      oD[i] = dot(b2, Tq) * rsqrt_r(dot(b2, b2));
+      oL[i] = dot(b1, F) * rsqrt_bond(dot(b1, b1));
+      oA[i] = dot(n, Tq) * rsqrt_bond(dot(n, n));
+      oD[i] = dot(b2, Tq) * rsqrt_bond(dot(b2, b2));
     }
   }
   if (tid == 0) {
@@ -661,9 +666,9 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
     const V3<R> b1 = x2 - x1;
     const V3<R> b0 = x1 - x0;
     const V3<R> n = cross(b1, b0);
-    gLr[1] = narrow<T>(dot(b1, F) * rsqrt_r(dot(b1, b1)));
-    gAr[0] = narrow<T>(dot(n, Tq) * rsqrt_r(dot(n, n)));
-    gLr[0] = narrow<T>(dot(b0, F + g1) * rsqrt_r(dot(b0, b0)));
+    gLr[1] = narrow<T>(dot(b1, F) * rsqrt_bond(dot(b1, b1)));
+    gAr[0] = narrow<T>(dot(n, Tq) * rsqrt_bond(dot(n, n)));
+    gLr[0] = narrow<T>(dot(b0, F + g1) * rsqrt_bond(dot(b0, b0)));
   }
   {
     const int o0 = Lay::lane_point_base(tid);
@@ -791,7 +796,7 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
       m = fmin(m, wave_stat[w][1]);
       xm = fmax(xm, wave_stat[w][2]);
     }
-    regular = regular && xm <= static_cast<R>(Fast::kScale) * m;
+    regular = regular && xm <= static_cast<R>(Fast::kScale) * m && m >= static_cast<R>(Fast::kMinLength);
   }
   if (regular) {
     const int o0 = Lay::lane_point_base(tid);

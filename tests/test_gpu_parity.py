@@ -480,6 +480,23 @@ def test_far_chain_is_not_regular_in_fp32(cufk, device):
     assert reg.cpu().tolist() == [0, 0]
 
 
+def test_tiny_chain_is_not_regular_in_fp32(cufk, device):
+    """Bonds below 2^-20 keep float32 chains off the position-based adjoint (whose bare
+    reciprocal square roots need normal inputs); the exact path still matches the oracle."""
+    lib = _abi()
+    d = _inputs(3, 60, seed=28, anchors=False, dtype=torch.float32)
+    d["lengths"][1] = _round(d["lengths"][1] * 4e-6, torch.float32)  # about 6e-7 < 2^-20
+    L, A, D = (_dev(d[k], torch.float32, device) for k in ("lengths", "angles", "dihedrals"))
+    an = _anchors3(d, torch.float32, device)
+    _, reg = _flagged_forward(lib, L, A, D, an)
+    assert reg.cpu().tolist() == [1, 0, 1]
+    _, grads = _run(cufk, d, torch.float32, device)
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    for got, want in zip(grads, ref):
+        err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
+        assert err.max() <= 2e-4, err
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("N", [4, 5, 70, 259, 1028, 2049, 2051])
 def test_fast_and_exact_backward_agree(cufk, device, dtype, N):
