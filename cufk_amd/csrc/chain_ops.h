@@ -304,8 +304,6 @@ __device__ __forceinline__ float min_positive(float a, float b) {
 }
 __device__ __forceinline__ double min_positive(double a, double b) { return fmin(a, b); }
 
-__device__ __forceinline__ float sqrt_r(float x) { return sqrtf(x); }
-__device__ __forceinline__ double sqrt_r(double x) { return sqrt(x); }
 __device__ __forceinline__ float rsqrt_r(float x) { return rsqrtf(x); }
 __device__ __forceinline__ double rsqrt_r(double x) { return rsqrt(x); }
 // 1/sqrt(x) for the position-based adjoint, whose regularity test keeps x normal: the bare

@@ -1,8 +1,11 @@
 // Torsion-only kernels (reference: src/cufk/csrc/torsion.cu).
 //
 // Step k uses bond length l[(k+2)%3], bond angle (k+1)%3 and the normalised raw pair k
-// (torsion.cu:67-73, 119-141).  K is a multiple of 12: lane segments are whole 16-byte groups
-// and every lane's item i has phase i % 3.
+// (torsion.cu:67-73, 119-141).  K is a multiple of 12: every lane's item i has phase i % 3.
+// The forward stages its rows with one pad word per lane (Layout Pad = 1): against Pad = 4
+// it needs 81 instead of 97 VGPRs and 9.6 instead of 10.3 KB of LDS at (1, 12), so 16
+// workgroups share a CU instead of 15 (at C3, 8192 chains fill two rounds of 16 per CU
+// exactly), and measured 29.9 against 33.9 us.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
                                                                  TorsionArgs cst, T* __restrict__ xyz, int points) {
   static_assert(K % 12 == 0, "torsion plans keep phases lane-invariant and segments 16-byte aligned");
   using R = compute_t<T>;
-  using Lay = Layout<W, K>;
+  using Lay = Layout<W, K, 1>;
   constexpr int kStage = 2 * Lay::kStepRow > Lay::kPointRow ? 2 * Lay::kStepRow : Lay::kPointRow;
   __shared__ __align__(16) R stage[kStage];
   __shared__ R wave_total[W][12];
