@@ -628,8 +628,9 @@ template <int W> __device__ __forceinline__ bool block_any(bool v, int (&flags)[
 }
 
 // ------------------------------------------------------------------ lane exchanges
-// Every exchange across lanes is a DPP move (or a v_readlane): __shfl_* compiles to
-// ds_bpermute plus VALU instructions for the lane address, and waits on an LDS round trip.
+// Every exchange across lanes is a DPP move or a v_readlane (the packed kernels' group
+// reductions use ds_swizzle): __shfl_* compiles to ds_bpermute plus VALU instructions for the
+// lane address, and waits on an LDS round trip.
 
 constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
 constexpr int kWaveShl1 = 0x130, kWaveShr1 = 0x138;
