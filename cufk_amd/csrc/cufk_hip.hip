@@ -319,7 +319,7 @@ int64_t cufk_long_segment_steps(int64_t batch, int64_t points) {
 
 int64_t cufk_long_state_doubles(int64_t batch, int64_t points, int64_t segment_steps) {
   if (check_long(batch, points, segment_steps) != CUFK_OK) return -1;
-  return batch * long_segments(points, segment_steps) * kLongStateDoubles;
+  return long_state_size(batch, points, long_segments(points, segment_steps));
 }
 
 int64_t cufk_long_work_doubles(int64_t batch, int64_t points, int64_t segment_steps) {

@@ -30,6 +30,15 @@ constexpr int64_t kLongTargetGroups = 1024;
 constexpr int64_t kLongMaxGroups = int64_t{UINT32_MAX} / 256;
 
 inline int64_t long_segments(int64_t points, int64_t seg_steps) { return (points - 3 + seg_steps - 1) / seg_steps; }
+// The state buffer: the per-(chain, segment) records, one flag byte per (chain, segment)
+// rounded up to 16 bytes, then the local positions, room for (batch, points, 3) doubles.
+inline int64_t long_flag_offset(int64_t batch, int64_t segs) { return batch * segs * kLongStateDoubles; }
+inline int64_t long_local_offset(int64_t batch, int64_t segs) {
+  return long_flag_offset(batch, segs) + (batch * segs + 15) / 16 * 2;
+}
+inline int64_t long_state_size(int64_t batch, int64_t points, int64_t segs) {
+  return long_local_offset(batch, segs) + batch * points * 3;
+}
 
 // Short chains: G lanes per chain, 8 steps per lane, several chains per workgroup (packed
 // kernels).  Measured on MI355X against one chain per workgroup: packing wins from about 4096

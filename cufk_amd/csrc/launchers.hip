@@ -324,9 +324,11 @@ template <typename T>
 int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, double* state,
                    int64_t B, int N, int S, hipStream_t st) {
   const int segs = static_cast<int>(long_segments(N, S));
+  uint8_t* const flags = reinterpret_cast<uint8_t*>(state + long_flag_offset(B, segs));
+  T* const local = reinterpret_cast<T*>(state + long_local_offset(B, segs));
   const int rc = with_scan_plan(S, [&]<int W, int K>() {
     hipLaunchKernelGGL((long_forward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
-                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, state, N, S, segs);
+                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, local, flags, state, N, S, segs);
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
   });
   if (rc != CUFK_OK) return rc;
@@ -335,7 +337,7 @@ int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
                      dim3(kLongThreads), 0, st, L, A, p0, fd, n0, state, B, N, segs);
   if (segs > 1)
     hipLaunchKernelGGL(long_forward_place_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
-                       st, xyz, state, N, S, segs);
+                       st, xyz, local, state, N, S, segs);
   return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
 }
 
@@ -344,6 +346,8 @@ int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
                    const double* state, const T* g, double* work, T* gL, T* gA, T* gD, int64_t B, int N, int S,
                    hipStream_t st) {
   const int segs = static_cast<int>(long_segments(N, S));
+  const uint8_t* const flags = reinterpret_cast<const uint8_t*>(state + long_flag_offset(B, segs));
+  const T* const local = reinterpret_cast<const T*>(state + long_local_offset(B, segs));
   if (segs > 1)
     hipLaunchKernelGGL(long_backward_sums_kernel<T>, dim3(static_cast<unsigned>(B * (segs - 1))), dim3(kLongThreads), 0,
                        st, xyz, g, state, work, N, S, segs);
@@ -353,7 +357,8 @@ int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
   if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
   return with_scan_plan(S, [&]<int W, int K>() {
     hipLaunchKernelGGL((long_backward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
-                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, g, gL, gA, gD, state, work, N, S, segs);
+                       dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, local, flags, g, gL, gA, gD, state, work, N,
+                       S, segs);
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
   });
 }

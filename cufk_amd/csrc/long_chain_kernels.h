@@ -16,8 +16,13 @@
 //   [0..5]   F = sum g and M = sum (x - x2) x g over the segment's own points
 //   [6..11]  the same sums over every point after the segment, about the segment's x2
 //
+// The state buffer then holds, after its records, one flag byte per (chain, segment) (the
+// forward's regularity test on the segment's own positions) and the local positions of
+// segments j >= 1 (a (points, 3) row of T per chain).
+//
 // Forward: segments (identity frame for j >= 1, local positions) -> frames -> place.
-// Backward: sums (saved positions) -> carry -> segments (exact adjoint with frame and carry).
+// Backward: sums (saved positions) -> carry -> segments (position-based adjoint over the local
+// positions where the flags allow it, else the exact adjoint with frame and carry).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -58,13 +63,15 @@ template <typename T, int W, int K, int Pad>
 __global__ __launch_bounds__(64 * W) void long_forward_segments_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
-    T* __restrict__ xyz, double* __restrict__ state, int points, int seg_steps, int segments) {
+    T* __restrict__ xyz, T* __restrict__ local, uint8_t* __restrict__ flags, double* __restrict__ state, int points,
+    int seg_steps, int segments) {
   const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 0);
   const int64_t b = s.chain;
+  const int64_t at = b * segments + s.index;
+  T* const out = (s.index == 0 ? xyz : local) + (b * points + s.first) * 3;
   forward_chain<T, Layout<W, K, Pad>, true>(
       lengths + b * (points - 1) + s.first, angles + b * (points - 2) + s.first, dihedrals + b * (points - 3) + s.first,
-      p0, first_direction, initial_normal, xyz + (b * points + s.first) * 3, nullptr, s.steps + 3, s.index == 0,
-      state + (b * segments + s.index) * kLongStateDoubles);
+      p0, first_direction, initial_normal, out, flags + at, s.steps + 3, s.index == 0, state + at * kLongStateDoubles);
 }
 
 // One wave per chain: the world frame at every segment's x2, composed in double from the
@@ -118,9 +125,10 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
   }
 }
 
-// Segments j >= 1: local positions y -> x2 + F y in world coordinates, in place.
+// Segments j >= 1: local positions y -> x2 + F y in world coordinates.
 template <typename T>
 __global__ __launch_bounds__(kLongThreads) void long_forward_place_kernel(T* __restrict__ xyz,
+                                                                         const T* __restrict__ local,
                                                                          const double* __restrict__ state, int points,
                                                                          int seg_steps, int segments) {
   const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 1);
@@ -131,10 +139,11 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_place_kernel(T* __r
 #pragma unroll
   for (int i = 0; i < 3; ++i) o[i] = f[9 + i];
   T* x = xyz + (s.chain * points + s.first + 3) * 3;
+  const T* y = local + (s.chain * points + s.first + 3) * 3;
   for (int i = threadIdx.x; i < s.steps; i += kLongThreads) {
-    const double y0 = static_cast<double>(widen(x[3 * i]));
-    const double y1 = static_cast<double>(widen(x[3 * i + 1]));
-    const double y2 = static_cast<double>(widen(x[3 * i + 2]));
+    const double y0 = static_cast<double>(widen(y[3 * i]));
+    const double y1 = static_cast<double>(widen(y[3 * i + 1]));
+    const double y2 = static_cast<double>(widen(y[3 * i + 2]));
 #pragma unroll
     for (int r = 0; r < 3; ++r)
       x[3 * i + r] = narrow<T>(static_cast<compute_t<T>>(o[r] + m[3 * r] * y0 + m[3 * r + 1] * y1 + m[3 * r + 2] * y2));
@@ -234,12 +243,14 @@ template <typename T, int W, int K, int Pad>
 __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ xyz, const T* __restrict__ local, const uint8_t* __restrict__ flags,
     const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
     T* __restrict__ grad_dihedrals, const double* __restrict__ state, const double* __restrict__ work, int points,
     int seg_steps, int segments) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
-  __shared__ __align__(16) R pstage[3 * Lay::kStepRow];
+  constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
+  __shared__ __align__(16) R pstage[kA];
   __shared__ __align__(16) R gstage[Lay::kPointRow];
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
@@ -247,6 +258,21 @@ __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
   const SegmentOf s = segment_of(blockIdx.x, points, seg_steps, segments, 0);
   const int64_t b = s.chain;
   const int64_t at = b * segments + s.index;
+  const bool head = s.index == 0;
+  // Position-based adjoint where this segment and the one before it (which holds the bond
+  // x1-x2) passed the forward's tests on their own positions.
+  if (FastPath<T>::kEnabled && flags[at] != 0 && (head || flags[at - 1] != 0)) {
+    const int64_t row = (b * points + s.first) * 3;
+    R* const dst[2] = {pstage, gstage};
+    const T* const src[2] = {(head ? xyz : local) + row, grad_xyz + row};
+    load_point_rows<Lay, 2>(dst, src, s.steps + 3, threadIdx.x);
+    __syncthreads();
+    position_adjoint<T, Lay, true>(grad_lengths + b * (points - 1) + s.first, grad_angles + b * (points - 2) + s.first,
+                                   grad_dihedrals + b * (points - 3) + s.first, pstage, gstage, wave_sum, s.steps + 3,
+                                   nullptr, head, state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6,
+                                   head ? R(0) : widen(lengths[b * (points - 1) + s.first + 1]));
+    return;
+  }
   exact_chain<T, Lay, true>(lengths + b * (points - 1) + s.first, angles + b * (points - 2) + s.first,
                             dihedrals + b * (points - 3) + s.first, p0, first_direction, initial_normal,
                             grad_xyz + (b * points + s.first) * 3, grad_lengths + b * (points - 1) + s.first,

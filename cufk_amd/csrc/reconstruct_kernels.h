@@ -339,9 +339,14 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   if (regular != nullptr && tid == 0) {
     bool reg = false;
     if constexpr (Fast::kEnabled) {
-      reg = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= Fast::kSinMin;
-      R m = fmin(ff.L0, ff.L1);
-      R x = abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2);
+      // A segment after the head has no first frame: its own steps and local positions only.
+      R m = R(1.0e30), x = R(0);
+      reg = true;
+      if (!Segmented || head) {
+        reg = ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= Fast::kSinMin;
+        m = fmin(ff.L0, ff.L1);
+        x = abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2);
+      }
 #pragma unroll
       for (int w = 0; w < W; ++w) {
         reg = reg && wave_stat[w][0] != R(0);
@@ -587,11 +592,22 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 // LDS for a coalesced store.
 // The adjoint above once positions (xs) and gradients (gs) sit in LDS point rows, visible to
 // the whole workgroup.
-template <typename T, typename Lay>
+//
+// Segmented: the rows are a segment of a longer chain (as in exact_chain).  carry[0..5] holds
+// F and M (about the segment's x2, world axes) of every point after the segment.  The head
+// segment holds world positions.  A later segment holds positions local to its x2, whose
+// world rotation is frame[0..8] (row-major): there x2 is the origin, x1 = (-bond1, 0, 0) for
+// the bond x1-x2 (the running frame's first axis is the bond into its origin), and the
+// gradients and the carry are turned to the local axes; only the head writes the
+// first-frame terms.
+template <typename T, typename Lay, bool Segmented = false>
 __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                  compute_t<T>* xs, compute_t<T>* gs,
                                                  compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
-                                                 double* __restrict__ anchor = nullptr) {
+                                                 double* __restrict__ anchor = nullptr, bool head = true,
+                                                 const double* __restrict__ frame = nullptr,
+                                                 const double* __restrict__ carry = nullptr,
+                                                 compute_t<T> bond1 = 0) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -623,6 +639,26 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
 #pragma unroll
     for (int i = 0; i < 3 * K; ++i) xr[9 + i] = xs[o0 + i];
   }
+  double q[9];  // Segmented, after the head: the world rotation at x2
+  if constexpr (Segmented) {
+    if (!head) {
+#pragma unroll
+      for (int i = 0; i < 9; ++i) q[i] = frame[i];
+      c = {R(0), R(0), R(0)};
+      if (tid == 0) {  // points 0..2 of the row belong to the previous segment
+#pragma unroll
+        for (int i = 0; i < 9; ++i) xr[i] = R(0);
+        xr[3] = -bond1;
+      }
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const R g0 = gr[3 * i], g1 = gr[3 * i + 1], g2 = gr[3 * i + 2];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          gr[3 * i + k] = static_cast<R>(q[k]) * g0 + static_cast<R>(q[3 + k]) * g1 + static_cast<R>(q[6 + k]) * g2;
+      }
+    }
+  }
   auto pos = [&](int j) { return V3<R>{xr[3 * j], xr[3 * j + 1], xr[3 * j + 2]} - c; };
 
   ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
@@ -638,6 +674,17 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
 
   // Reverse walk: item i is point p = 3+s0+i (xr index i+3) with neighbours i+2, i+1.
   V3<R> F = tail.f, M = tail.m;
+  if constexpr (Segmented) {
+    V3<double> cf = {carry[0], carry[1], carry[2]}, cm = {carry[3], carry[4], carry[5]};
+    if (!head) {
+      cf = {q[0] * cf.x + q[3] * cf.y + q[6] * cf.z, q[1] * cf.x + q[4] * cf.y + q[7] * cf.z,
+            q[2] * cf.x + q[5] * cf.y + q[8] * cf.z};
+      cm = {q[0] * cm.x + q[3] * cm.y + q[6] * cm.z, q[1] * cm.x + q[4] * cm.y + q[7] * cm.z,
+            q[2] * cm.x + q[5] * cm.y + q[8] * cm.z};
+    }
+    F = F + V3<R>{static_cast<R>(cf.x), static_cast<R>(cf.y), static_cast<R>(cf.z)};
+    M = M + V3<R>{static_cast<R>(cm.x), static_cast<R>(cm.y), static_cast<R>(cm.z)};
+  }
   R oL[K], oA[K], oD[K];
 #pragma unroll
   for (int i = K - 1; i >= 0; --i) {
@@ -655,7 +702,7 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
       oD[i] = dot(b2, Tq) * rsqrt_bond(dot(b2, b2));
     }
   }
-  if (tid == 0) {
+  if (tid == 0 && (!Segmented || head)) {
     // Atoms 2 and 1: dL/dL[1], dL/dA[0] and dL/dL[0]; x2 is the origin, so M_2 = M_3.
     const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
     const V3<R> g1 = load3(&gs[3]);

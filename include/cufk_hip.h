@@ -201,8 +201,12 @@ int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles
  * one workgroup, joined by short per-chain passes in double.  The caller provides two float64
  * buffers: `state` (cufk_long_state_doubles elements), written by the forward and read by the
  * backward of the same inputs and segment_steps; and `work` (cufk_long_work_doubles
- * elements), scratch for the backward.  Neither needs initialising.  The backward takes the
- * forward's xyz and applies the exact adjoint in every segment.
+ * elements), scratch for the backward.  Neither needs initialising.  Besides the per-segment
+ * records, `state` holds the local positions of every segment after the first and a flag per
+ * segment (the forward's regularity test on its own positions), so it is sized for
+ * (batch, points, 3) doubles more.  The backward takes the forward's xyz and state: the
+ * position-based adjoint over the local positions in flagged segments (whose predecessor is
+ * flagged too), the exact adjoint in the others.
  */
 /* Default segment length for (batch, points): 2048, halved (down to 256) while the grid would
  * hold fewer than 1024 segments.  0 for invalid shapes. */

@@ -173,10 +173,11 @@ def test_long_sizes_and_default_segments(lib):
     assert seg(64, 131072) == 2048  # 64 x 64 segments
     assert seg(16, 65536) == 1024  # 16 x 32 = 512 < 1024 at 2048; 16 x 64 at 1024
     assert seg(0, 10) == 256 and seg(4, 3) == 0 and seg(-1, 10) == 0
-    # state: 24 doubles, work: 12 doubles per (chain, segment); segments = ceil((N-3)/S)
-    assert lib.cufk_long_state_doubles(3, 5003, 1000) == 3 * 5 * 24
+    # 24 doubles per (chain, segment), its flag bytes in whole 16-byte units, then room for
+    # the local positions as (chains, points, 3) doubles.
+    assert lib.cufk_long_state_doubles(3, 5003, 1000) == 3 * 5 * 24 + 2 + 3 * 5003 * 3
     assert lib.cufk_long_work_doubles(3, 5003, 1000) == 3 * 5 * 12
-    assert lib.cufk_long_state_doubles(3, 5004, 1000) == 3 * 6 * 24
+    assert lib.cufk_long_state_doubles(3, 5004, 1000) == 3 * 6 * 24 + 4 + 3 * 5004 * 3
     assert lib.cufk_long_state_doubles(3, 5004, 0) == -1
     assert lib.cufk_long_state_doubles(3, 5004, 2049) == -1
     assert lib.cufk_long_state_doubles(3, 3, 16) == -1

@@ -143,7 +143,8 @@ def test_long_fp64_gradcheck(cufk, device):
 
 def test_long_irregular_chains(cufk, device):
     """Negative and zero bonds, bond angles near 0 and pi, inside non-head segments and at
-    segment boundaries: the exact adjoint holds everywhere (float32 bar 2e-4 relative)."""
+    segment boundaries: the segments they touch take the exact adjoint, the others the
+    position-based one (float32 bar 2e-4 relative)."""
     d = _inputs(4, 400, seed=11, anchors=True, dtype=torch.float32)
     d["lengths"][0, 130] *= -1  # inside segment 2 (steps 128..191 place points 131..)
     d["lengths"][1, 66] = 0.0  # first step of segment 1 uses L[66]
@@ -155,6 +156,24 @@ def test_long_irregular_chains(cufk, device):
     mx = np.abs(xyz.detach().double().cpu().numpy() - ref_x).max()
     print(f"fp32 long irregular: forward max err {mx:.3e}")
     assert mx <= 1e-4
+    for got, want in zip(grads, ref_g):
+        err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
+        print("  per-chain grad rel err", err)
+        assert err.max() <= 2e-4
+
+
+def test_long_position_adjoint_far_anchor_and_boundary_bonds(cufk, device):
+    """The position-based adjoint of later segments runs over positions local to each
+    segment, so an anchor 90 nm from the origin (which sends the head segment to the
+    exact adjoint) leaves the later segments at the float32 bar; a zero bond x1-x2 of a later
+    segment (a step of the segment before it) sends that segment to the exact adjoint too."""
+    d = _inputs(4, 1500, seed=21, anchors=True, dtype=torch.float32)
+    d["p0"] = np.array([60.0, -40.0, 50.0])
+    d["lengths"][1, 129] = 0.0  # segment 2 (steps 128..) has x1-x2 = L[129], from step 127
+    d["lengths"][2, 257] = 1.0e-7  # below the float32 minimum bond: segments 3 and 4 exact
+    d = {k: _round(v, torch.float32) for k, v in d.items()}
+    xyz, grads = _run_long(cufk, d, torch.float32, device, 128)
+    ref_x, ref_g = _ref(d)
     for got, want in zip(grads, ref_g):
         err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
         print("  per-chain grad rel err", err)
