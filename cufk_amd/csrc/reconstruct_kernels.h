@@ -600,14 +600,17 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 // the bond x1-x2 (the running frame's first axis is the bond into its origin), and the
 // gradients and the carry are turned to the local axes; only the head writes the
 // first-frame terms.
-template <typename T, typename Lay, bool Segmented = false>
+//
+// Residual: gs holds a target row and the gradient is w2 (x - target), formed as the lane
+// loads its points (the coordinate loss's backward).
+template <typename T, typename Lay, bool Segmented = false, bool Residual = false>
 __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                  compute_t<T>* xs, compute_t<T>* gs,
                                                  compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
                                                  double* __restrict__ anchor = nullptr, bool head = true,
                                                  const double* __restrict__ frame = nullptr,
                                                  const double* __restrict__ carry = nullptr,
-                                                 compute_t<T> bond1 = 0) {
+                                                 compute_t<T> bond1 = 0, compute_t<T> w2 = 0) {
   using R = compute_t<T>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
@@ -638,6 +641,10 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
     }
 #pragma unroll
     for (int i = 0; i < 3 * K; ++i) xr[9 + i] = xs[o0 + i];
+    if constexpr (Residual) {
+#pragma unroll
+      for (int i = 0; i < 3 * K; ++i) gr[i] = w2 * (xr[9 + i] - gr[i]);
+    }
   }
   double q[9];  // Segmented, after the head: the world rotation at x2
   if constexpr (Segmented) {
@@ -705,9 +712,14 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
   if (tid == 0 && (!Segmented || head)) {
     // Atoms 2 and 1: dL/dL[1], dL/dA[0] and dL/dL[0]; x2 is the origin, so M_2 = M_3.
     const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
-    const V3<R> g1 = load3(&gs[3]);
-    const V3<R> g2 = load3(&gs[6]);
-    if (anchor != nullptr) store_anchor_sums(anchor, F, M, x0, x1, load3(&gs[0]), g1, g2);
+    auto grad = [&](int j) {
+      const V3<R> g = load3(&gs[3 * j]);
+      if constexpr (Residual) return w2 * (load3(&xs[3 * j]) - g);
+      return g;
+    };
+    const V3<R> g1 = grad(1);
+    const V3<R> g2 = grad(2);
+    if (anchor != nullptr) store_anchor_sums(anchor, F, M, x0, x1, grad(0), g1, g2);
     F = F + g2;
     const V3<R> Tq = M - cross(x1, F);
     const V3<R> b1 = x2 - x1;
@@ -1045,17 +1057,18 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
   }
   __syncthreads();
   const R w2 = R(2) * (grad_loss != nullptr ? widen(grad_loss[row]) : R(1));
-  for (int e = tid; e < 3 * points; e += Lay::kLanes) {
-    const int slot = Lay::point_slot(e);
-    region_b[slot] = w2 * (region_a[slot] - region_b[slot]);
-  }
-  __syncthreads();
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
   T* gDr = grad_dihedrals + row * (points - 3);
   if (FastPath<T>::kEnabled && regular[row] != 0) {
-    position_adjoint<T, Lay>(gLr, gAr, gDr, region_a, region_b, wave_sum, points);
+    position_adjoint<T, Lay, false, true>(gLr, gAr, gDr, region_a, region_b, wave_sum, points, nullptr, true, nullptr,
+                                          nullptr, R(0), w2);
   } else {
+    for (int e = tid; e < 3 * points; e += Lay::kLanes) {
+      const int slot = Lay::point_slot(e);
+      region_b[slot] = w2 * (region_a[slot] - region_b[slot]);
+    }
+    __syncthreads();
     exact_chain<T, Lay, false, false>(lengths + row * (points - 1), angles + row * (points - 2),
                                       dihedrals + row * (points - 3), p0, first_direction, initial_normal, nullptr, gLr,
                                       gAr, gDr, region_a, region_b, wave_total, wave_sum, wide_vote, points);
