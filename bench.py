@@ -6,30 +6,37 @@ chains (config 2 draws: lengths ~N(0.145, 0.01) clipped to [0.12, 0.17], angles 
 already resident in HBM.  The step runs through the public autograd API
 (``reconstruct`` + ``torch.autograd.grad``).
 
-The default 1000 warm-up steps (about 0.1 s of GPU work at config 2) bring the GPU to its
-steady clocks: after only 10 warm-up steps the first 50 timed steps run about 20 % slower.
-The timed steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB
-at config 2), so no step finds its inputs in the 256 MB last-level cache left behind by the
-previous one.  HIP events recorded inside the timed region on the stream the kernels run on
-(the current torch stream, which the extension launches on) bracket the K timed steps; a second
-pass of K steps puts events around each step's forward call and around its backward node
-(autograd pre- and post-hooks), which splits the step.  ``roofline`` is for the backward: its
-algorithmic bytes per launch are 4*B*(9N-12) (read lengths, angles, dihedrals and grad_xyz,
-write the three gradients), divided by the backward node's average duration over that second
-pass (the kernel as the timed steps run it, which is what rocprofv3's kernel trace of the same
-command averages), against MI355X's 8 TB/s HBM peak.  ``traffic`` is the HBM bytes per launch
-the rocprofv3 FETCH_SIZE and WRITE_SIZE counters read for the same kernel, copied from the
-committed summaries under profiles/ (MEASURED_TRAFFIC below).  ``abi_*_us`` time each C-ABI
-entry point alone over back-to-back launches rotating over the input sets (an event pair per
-launch); a backward launched after another backward, not after its forward, no longer finds the
-forward's output in the last-level cache, so those run slower than in the step.
+Order of work:
+1. Clock ramp: steps are run for ``--ramp-s`` seconds (0.5 s by default) before the W warm-up
+   steps, so a short ``--warmup`` still times the GPU at its steady clocks (after only a few
+   warm-up steps the first 50 timed steps run about 20 % slower).  Reported as
+   ``config.ramp_steps``; none of it is timed.
+2. W warm-up steps, then the K timed steps back to back, bracketed by synchronize and a pair of
+   HIP events on the stream the kernels run on: ``ms_per_step`` and ``value`` = B*N / step.
+   The steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB at
+   config 2), so no step finds its inputs in the 256 MB last-level cache.
+3. Forward only: K forward calls without autograd, timed the same way (``forward_atoms_per_s``).
+4. Kernel split: K back-to-back launches of the forward entry point the step uses (the flagged
+   forward, through the C ABI) under one event pair give ``kernels.forward_us``; the backward
+   is the step minus that, so the two add up to the step.  (An event pair around each launch
+   would add a few microseconds per launch on this part.)
+5. ``--abi-reps`` back-to-back launches of each C-ABI entry point the step uses (0 by default).
 
-The CPU baseline is the float64 numpy oracle (oracle/nerf64.py) run on this host on a bounded
-sample of chains of the same shape (chunks of about 128 x 2049 points until about 15 s of work),
-scaled to atoms/s.
+``roofline`` is for the step, the metric's own quantity: (forward + backward algorithmic bytes)
+/ ms_per_step against MI355X's 8 TB/s HBM peak.  Algorithmic bytes per chain: forward s(6N-6)
+(read lengths, angles, dihedrals; write xyz), backward s(9N-12) (read the three parameter rows'
+worth and grad_xyz; write the three gradients).  ``traffic`` is what rocprofv3's FETCH_SIZE and
+WRITE_SIZE counters read for the two kernels, per step (MEASURED_TRAFFIC below, copied from the
+committed summaries under profiles/).  ``kernels`` splits the step: forward and backward
+durations from pass 4 and each one's fraction of the HBM peak.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss]
-                    [--graph]
+The CPU baseline is the reference algorithm on this host's cores: serial float64 NeRF
+(forward, then the explicit reverse adjoint) in PyTorch CPU (oracle/cpu_torch.py), vectorised
+over the chains with torch's intra-op threads, the median of 3 runs over the config's batch (or
+a subset of it where one run would take longer than about 20 s), scaled to atoms/s.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+                    [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss] [--graph]
 
 With --graph each input set's step is captured once in a HIP graph (torch.cuda.graph) and the
 timed steps replay the graphs: the kernels are the same, the per-step Python, autograd-engine and
@@ -70,11 +77,11 @@ BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
 DTYPE_CODES = {"float32": 0, "float64": 1, "float16": 2, "bfloat16": 3}
 ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by what the
-# counter reads for a plain copy of known size; see profiles/reconstruct_c2_hbm_traffic.md.
-# Keyed by (config, kernel); a missing entry reports traffic as null.
+# HBM bytes per step (forward + backward launch) from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+# each counter scaled by what it reads for a plain copy of known size; the per-kernel figures are
+# in profiles/reconstruct_c2_hbm_traffic.md.  A config without an entry reports traffic as null.
 MEASURED_TRAFFIC = {
-    ("c2", "reconstruct_backward"): 303494325,  # 202665849 read (xyz, grad_xyz) + 100828476 written
+    "c2": 203211803 + 303489063,  # forward (read 102350363, write 100861440) + backward (202659879 + 100829184)
 }
 
 
@@ -82,15 +89,18 @@ def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=500)
-    p.add_argument("--warmup", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--ramp-s", type=float, default=0.5,
+                   help="seconds of untimed steps before the warm-up steps (GPU clock ramp)")
     p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    p.add_argument("--kernel-reps", type=int, default=200)
+    p.add_argument("--abi-reps", type=int, default=0,
+                   help="back-to-back launches of each C-ABI entry point to time (0 = skip)")
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--graph", action="store_true",
                    help="capture each input set's step (forward + torch.autograd.grad) in a HIP graph and time replays")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-sample", type=int, default=0, help="chains in the CPU sample (0 = about 15 s of work)")
-    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-runs", type=int, default=3, help="CPU baseline runs (the median is reported)")
+    p.add_argument("--cpu-seconds", type=float, default=20.0, help="rough cap on one CPU baseline run")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     return p.parse_args()
@@ -124,19 +134,19 @@ def synthetic(B, N, seed, torch, device, dtype):
 
 
 def event_time_ms(torch, fn, reps):
-    """Average duration of fn(i) over reps back-to-back calls (i = 0..reps-1): a pair of HIP
-    events on the current stream brackets each call, so the average is the launch's own
-    duration (what rocprofv3's kernel trace reports), without the gaps between launches."""
+    """Average time per call of fn(i) over reps back-to-back calls (i = 0..reps-1), under one
+    pair of HIP events on the current stream: each call's own duration plus the short gap
+    between launches (an event pair around each call would add a few microseconds per call)."""
     stream = torch.cuda.current_stream()
-    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     fn(0)
     torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
     for i in range(reps):
-        marks[i][0].record(stream)
         fn(i)
-        marks[i][1].record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in marks) / reps
+    return a.elapsed_time(b) / reps
 
 
 def coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device, chains=64):
@@ -165,45 +175,68 @@ def coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device, chains=64
     }
 
 
-def cpu_baseline(kind, B, N, sample, seconds):
-    """Float64 oracle fwd + bwd on a bounded sample of chains, scaled to atoms/s.
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    Chains are processed in chunks of at most 128 (bounding memory).  With sample == 0,
-    chunks run until about `seconds` of work is done or B chains are covered; otherwise exactly
-    `sample` chains.  A 4-chain warm-up (1 chain for chains past 65k points) is not counted.
-    Returns (atoms/s, chains, wall seconds, cpu seconds)."""
+
+def cpu_baseline(torch, kind, B, N, runs, seconds):
+    """The reference algorithm on this host's CPU cores (oracle/cpu_torch.py): float64 forward
+    plus explicit reverse adjoint in PyTorch, vectorised over chains, serial over steps.
+
+    One small run estimates the cost per chain; the sample is then the config's whole batch or
+    the largest subset that keeps one run near `seconds`.  Returns the median atoms/s over
+    `runs` runs, the chain count, the per-run wall times and the thread count."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import nerf64 as o
+    from oracle import cpu_torch as ct
 
-    def chunk(n, seed):
+    threads = torch.get_num_threads()  # torch's intra-op pool: OMP_NUM_THREADS or the host's cores
+    gen = torch.Generator().manual_seed(1000)
+    consts = None
+    if kind == "torsion":
+        from oracle import nerf64 as o
+
+        consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+
+    def make(n):
         if kind == "torsion":
-            rng = np.random.default_rng(seed)
-            raw = rng.normal(size=(n, 2 * (N - 3)))
-            g = rng.normal(size=(n, N, 3))
-            c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
-            t0, c0 = time.perf_counter(), time.process_time()
-            x = o.torsion_forward(raw, c)
-            o.torsion_backward(raw, x, g, c)
-        else:
-            d = o.synthetic_inputs(n, N, seed=seed, anchors=True)
-            an = dict(p0=d["p0"], first_direction=d["first_direction"], initial_normal=d["initial_normal"])
-            t0, c0 = time.perf_counter(), time.process_time()
-            o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
-            o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **an)
-        return time.perf_counter() - t0, time.process_time() - c0
+            raw = torch.randn(n, 2 * (N - 3), generator=gen, dtype=torch.float64)
+            return raw, torch.randn(n, N, 3, generator=gen, dtype=torch.float64)
+        L = (torch.randn(n, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
+        A = torch.randn(n, N - 2, generator=gen, dtype=torch.float64) * 0.08 + 2.05
+        D = (torch.rand(n, N - 3, generator=gen, dtype=torch.float64) * 2 - 1) * np.pi
+        g = torch.randn(n, N, 3, generator=gen, dtype=torch.float64)
+        p0 = torch.randn(3, generator=gen, dtype=torch.float64)
+        q, _ = torch.linalg.qr(torch.randn(3, 3, generator=gen, dtype=torch.float64))
+        return L, A, D, g, p0, q[:, 0].contiguous(), q[:, 1].contiguous()
 
-    per_chunk = max(1, min(128, 128 * 2049 // N))  # about 128 x 2049 points per chunk
-    chunk(4 if per_chunk >= 4 else 1, 1000)
-    limit = sample if sample > 0 else B
-    wall = cpu = 0.0
-    done = 0
-    while done < limit and (sample > 0 or wall < seconds):
-        n = min(per_chunk, limit - done)
-        w, c = chunk(n, 2 + done)
-        wall += w
-        cpu += c
-        done += n
-    return done * N / wall, done, wall, cpu
+    def run(inputs):
+        t0 = time.perf_counter()
+        if kind == "torsion":
+            raw, g = inputs
+            x = ct.torsion_forward(raw, consts.lengths, consts.sin, consts.cos)
+            ct.torsion_backward(raw, x, g, consts.lengths)
+        else:
+            L, A, D, g, p0, fd, n0 = inputs
+            x = ct.forward(L, A, D, p0, fd, n0)
+            if kind == "loss":
+                g = 2.0 * (x - g * 0.3)  # the loss against the same target bench.py uses on the GPU
+            ct.backward(x, g)
+        return time.perf_counter() - t0
+
+    probe = max(1, min(B, 64))
+    est = run(make(probe)) / probe  # also warms torch's CPU kernels
+    n = int(max(1, min(B, seconds / max(est, 1e-9))))
+    inputs = make(n)
+    walls = sorted(run(inputs) for _ in range(max(1, runs)))
+    med = walls[len(walls) // 2]
+    return n * N / med, n, walls, threads
 
 
 def main():
@@ -235,7 +268,7 @@ def main():
     i64 = ctypes.c_int64
 
     # One entry per input set: the autograd step and the two C-ABI calls it makes.
-    steps, fwds, bwds, regular = [], [], [], []
+    steps, fwds, bwds, regular, fonly = [], [], [], [], []
     if kind == "long":
         # Algorithmic bytes as for reconstruct; the segment joins (placement, segment sums)
         # are extra traffic the roofline fraction is charged with.
@@ -253,10 +286,8 @@ def main():
             for t in (L, A, D):
                 t.requires_grad_(True)
 
-            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
+            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0):
                 xyz = cufk_amd.reconstruct_long(L, A, D, p0, fd, n0)
-                if mark is not None:
-                    mark(xyz)
                 return torch.autograd.grad(xyz, (L, A, D), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -277,6 +308,7 @@ def main():
 
             fwd(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))  # state for the ABI backward
             steps.append(step)
+            fonly.append(lambda L=L, A=A, D=D, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct_long(L, A, D, p0, fd, n0))
             fwds.append(fwd)
             bwds.append(bwd)
     elif kind == "loss":
@@ -292,10 +324,8 @@ def main():
             for t in (L, A, D):
                 t.requires_grad_(True)
 
-            def step(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, mark=None):
+            def step(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
                 loss = cufk_amd.reconstruct_loss(L, A, D, target, p0, fd, n0)
-                if mark is not None:
-                    mark(loss)
                 return torch.autograd.grad(loss.sum(), (L, A, D))
 
             def plain(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
@@ -321,6 +351,8 @@ def main():
             fwds.append(fwd)
             bwds.append(bwd)
             unfused.append(plain)
+            fonly.append(lambda L=L, A=A, D=D, t=target, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct_loss(L, A, D, t, p0,
+                                                                                                       fd, n0))
     elif kind == "reconstruct":
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
@@ -330,10 +362,8 @@ def main():
             A.requires_grad_(True)
             D.requires_grad_(True)
 
-            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0, mark=None):
+            def step(L=L, A=A, D=D, g=g, p0=p0, fd=fd, n0=n0):
                 xyz = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
-                if mark is not None:
-                    mark(xyz)
                 return torch.autograd.grad(xyz, (L, A, D), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -372,6 +402,7 @@ def main():
             fwds.append(fwd)
             bwds.append(bwd)
             regular.append(flags)
+            fonly.append(lambda L=L, A=A, D=D, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct(L, A, D, p0, fd, n0))
     else:
         import math
 
@@ -389,10 +420,8 @@ def main():
             g = torch.randn(B, N, 3, generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
             raw.requires_grad_(True)
 
-            def step(raw=raw, g=g, mark=None):
+            def step(raw=raw, g=g):
                 xyz = f(raw)
-                if mark is not None:
-                    mark(xyz)
                 return torch.autograd.grad(xyz, (raw,), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
@@ -410,6 +439,7 @@ def main():
             steps.append(step)
             fwds.append(fwd)
             bwds.append(bwd)
+            fonly.append(lambda raw=raw: f(raw))
 
     if args.graph:
         # One graph per input set: warm up on a side stream, capture, then the timed steps
@@ -430,13 +460,22 @@ def main():
             graphs.append(graph)
         steps = [graph.replay for graph in graphs]
 
+    stream = torch.cuda.current_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    # 1. Clock ramp (untimed), then 2. the W warm-up steps.
+    ramp_steps = 0
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < args.ramp_s:
+        for _ in range(10):
+            steps[ramp_steps % nsets]()
+            ramp_steps += 1
+        torch.cuda.synchronize()
     for i in range(args.warmup):
         steps[i % nsets]()
     torch.cuda.synchronize()
 
     # Timed region: K steps back to back on the stream the kernels run on.
-    stream = torch.cuda.current_stream()
-    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     t_start, t_end = ev(), ev()
     torch.cuda.synchronize()
     t_start.record(stream)
@@ -446,37 +485,39 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
 
-    # The same K steps again with events around each step's forward call and around its
-    # backward node (autograd pre- and post-hooks on the output's grad_fn, run on the same
-    # stream right before and after the node launches its kernel).  The extra event packets
-    # cost a little per step, so this pass is reported apart from ms_per_step.
-    marks = [(ev(), ev(), ev(), ev()) for _ in range(0 if args.graph else args.steps)]
+    # 3. Forward only: K forward calls without autograd (the plain forward kernels).
+    with torch.no_grad():
+        for i in range(min(args.warmup, 10)):
+            fonly[i % nsets]()
+        torch.cuda.synchronize()
+        f_start, f_end = ev(), ev()
+        f_start.record(stream)
+        for i in range(args.steps):
+            fonly[i % nsets]()
+        f_end.record(stream)
+        torch.cuda.synchronize()
+    ms_forward_only = f_start.elapsed_time(f_end) / args.steps
 
-    def marker(m):
-        def mark(out):
-            m[1].record(stream)
-            out.grad_fn.register_prehook(lambda grad_out: m[2].record(stream))
-            out.grad_fn.register_hook(lambda grad_in, grad_out: m[3].record(stream))
-
-        return mark
-
-    torch.cuda.synchronize()
-    for i in range(len(marks)):
-        marks[i][0].record(stream)
-        steps[i % nsets](mark=marker(marks[i]))
-    torch.cuda.synchronize()
-    seg_fwd = sum(m[0].elapsed_time(m[1]) for m in marks) / len(marks) if marks else None
-    seg_bwd = sum(m[2].elapsed_time(m[3]) for m in marks) / len(marks) if marks else None
-
-    # Kernel-level timing straight through the C ABI, rotating over the same sets.
+    # 4. Kernel split of the step: K launches of the step's own forward entry point (the flagged
+    # forward through the C ABI) back to back under one event pair, rotating over the same sets;
+    # the backward is the rest of the step.  Event pairs around single launches would not do:
+    # each event adds a few microseconds on this part.
     st = ctypes.c_void_p(stream.cuda_stream)
-    t_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.kernel_reps)
-    t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), args.kernel_reps)
+    for i in range(nsets):
+        fwds[i](st)  # also writes each set's regularity flags
+    seg_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.steps)
+    seg_bwd = ms_per_step - seg_fwd
+
+    # 5. Optional: each C-ABI entry point alone, back to back, rotating over the same sets.
+    t_fwd = t_bwd = None
+    if args.abi_reps > 0:
+        t_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.abi_reps)
+        t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), args.abi_reps)
     regular_frac = float(torch.stack(regular).float().mean()) if regular else None
 
     unfused_us = None
     if kind == "loss":  # the same step through reconstruct and a torch loss, same input sets
-        for i in range(args.warmup // 4):
+        for i in range(args.warmup):
             unfused[i % nsets]()
         torch.cuda.synchronize()
         u0, u1 = ev(), ev()
@@ -492,13 +533,11 @@ def main():
         precision = coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device)
 
     atoms = B * N
-    # The backward kernel as the timed steps run it; replayed graphs hold no events, so with
-    # --graph the C-ABI launches stand in.
-    bwd_ms = seg_bwd if seg_bwd is not None else t_bwd
-    fwd_ms = seg_fwd if seg_fwd is not None else t_fwd
-    bw_bwd = bwd_bytes / (bwd_ms * 1e-3) / 1e9
-    bw_fwd = fwd_bytes / (fwd_ms * 1e-3) / 1e9
-    traffic = MEASURED_TRAFFIC.get((args.config, f"{kind}_backward"))
+    step_bytes = fwd_bytes + bwd_bytes
+    gbs = lambda nbytes, ms: None if ms is None else nbytes / (ms * 1e-3) / 1e9  # noqa: E731
+    us = lambda ms: None if ms is None else ms * 1e3  # noqa: E731
+    frac = lambda nbytes, ms: None if ms is None else gbs(nbytes, ms) / HBM_PEAK_GBS  # noqa: E731
+    traffic = MEASURED_TRAFFIC.get(args.config)
     result = {
         "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
         "value": atoms / (ms_per_step * 1e-3),
@@ -514,26 +553,31 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{kind} fwd+bwd" + (", replayed HIP graph" if args.graph else ""),
                    "config": args.config, "batch": B, "points": N, "dtype": dtype_name, "anchors": "random",
-                   "input_sets": nsets},
+                   "input_sets": nsets, "ramp_steps": ramp_steps},
+        "forward_atoms_per_s": atoms / (ms_forward_only * 1e-3),
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{kind}_backward",
-            "achieved": bw_bwd,
+            "kernel": f"{kind} forward + backward (one step: the two launches the metric times)",
+            "achieved": gbs(step_bytes, ms_per_step),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": bw_bwd / HBM_PEAK_GBS,
+            "frac": frac(step_bytes, ms_per_step),
             "traffic": traffic,
-            "algorithmic_bytes": bwd_bytes,
-            "avg_launch_us": bwd_ms * 1e3,
+            "algorithmic_bytes": step_bytes,
+            "avg_step_us": ms_per_step * 1e3,
         },
         "kernels": {
-            "step_forward_us": seg_fwd * 1e3 if seg_fwd is not None else None,
-            "step_backward_us": seg_bwd * 1e3 if seg_bwd is not None else None,
-            "step_forward_GBs": bw_fwd,
-            "step_backward_GBs": bw_bwd,
-            "abi_forward_us": t_fwd * 1e3,
-            "abi_backward_us": t_bwd * 1e3,
-            "step_frac_of_hbm_peak": (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "forward_us": us(seg_fwd),
+            "backward_us": us(seg_bwd),
+            "split": "forward: K back-to-back launches of the step's forward entry point; backward: the step minus "
+                     "that (so it also holds the gaps between launches)",
+            "forward_frac": frac(fwd_bytes, seg_fwd),
+            "backward_frac": frac(bwd_bytes, seg_bwd),
+            "forward_algorithmic_bytes": fwd_bytes,
+            "backward_algorithmic_bytes": bwd_bytes,
+            "forward_only_us": ms_forward_only * 1e3,
+            "abi_forward_us": us(t_fwd),
+            "abi_backward_us": us(t_bwd),
             "regular_chain_fraction": regular_frac,
             "unfused_step_us": unfused_us,
         },
@@ -541,14 +585,17 @@ def main():
     if precision is not None:
         result["precision"] = precision
     if not args.no_cpu_baseline:
-        v, chains, wall, cpu = cpu_baseline(kind, B, N, args.cpu_sample, args.cpu_seconds)
+        v, chains, walls, threads = cpu_baseline(torch, kind, B, N, args.cpu_runs, args.cpu_seconds)
         result["cpu_baseline"] = {
             "value": v,
             "unit": "atoms/s",
-            "cores": max(1, round(cpu / wall)),
+            "cores": threads,
             "kind": "port",
-            "sample": f"float64 numpy oracle, fwd+bwd of {chains} chains x N={N} ({wall:.1f} s wall, "
-                      f"{cpu:.1f} s cpu), scaled to atoms/s",
+            "sample": f"serial float64 NeRF forward + reverse adjoint in PyTorch CPU (oracle/cpu_torch.py), "
+                      f"{chains} chains x N={N}, median of {len(walls)} runs "
+                      f"({', '.join(f'{w:.2f}' for w in walls)} s) on {threads} threads of {cpu_model()} "
+                      f"(host: {os.cpu_count()} logical CPUs, {len(os.sched_getaffinity(0))} in this process's "
+                      f"affinity), scaled to atoms/s",
         }
     print(json.dumps(result))
     return 0

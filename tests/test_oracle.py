@@ -371,3 +371,58 @@ def test_checks_catch_a_dropped_first_frame_gradient_term():
     dropped = gA[:, 0] - d["lengths"][:, 1] * np.sum(F2 * d_dir, -1)
     assert np.abs(gA[:, 0] - tA[:, 0]).max() < 1e-12
     assert np.abs(dropped - tA[:, 0]).max() > 1e-3
+
+
+# ------------------------------------------------------------------ the CPU baseline (PyTorch)
+
+
+def _torch_inputs(d):
+    return {k: torch.tensor(v, dtype=torch.float64) for k, v in d.items()}
+
+
+@pytest.mark.parametrize("N", [4, 5, 64, 300])
+def test_cpu_torch_baseline_matches_the_oracle(N):
+    """bench.py's CPU baseline (oracle/cpu_torch.py) equals the pinned float64 oracle: forward
+    within 1e-12, world-frame adjoint within 1e-10 relative of the reference-form backward."""
+    from oracle import cpu_torch as ct
+
+    d = o.synthetic_inputs(4, N, seed=50 + N, anchors=True)
+    t = _torch_inputs(d)
+    x = ct.forward(t["lengths"], t["angles"], t["dihedrals"], t["p0"], t["first_direction"], t["initial_normal"])
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchors(d))
+    assert np.abs(x.numpy() - ref).max() <= 1e-12
+    got = ct.backward(x, t["grad"])
+    want = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchors(d))
+    for a, b in zip(got, want):
+        assert np.abs(a.numpy() - b).max() <= 1e-10 * np.abs(b).max()
+
+
+@pytest.mark.parametrize("fd", [[0.0, 0.0, 2.0], [1.0, 0.1, 0.0]])
+def test_cpu_torch_baseline_degenerate_normal(fd):
+    from oracle import cpu_torch as ct
+
+    d = o.synthetic_inputs(2, 30, seed=8, anchors=True)
+    d["first_direction"] = np.array(fd)
+    d["initial_normal"] = np.array(fd) * -3.0
+    t = _torch_inputs(d)
+    x = ct.forward(t["lengths"], t["angles"], t["dihedrals"], t["p0"], t["first_direction"], t["initial_normal"])
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchors(d))
+    assert np.abs(x.numpy() - ref).max() <= 1e-12
+
+
+def test_cpu_torch_torsion_matches_the_oracle():
+    """Torsion forward and backward, with a zero pair and a pair below the 1e-8 clamp."""
+    from oracle import cpu_torch as ct
+
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    rng = np.random.default_rng(12)
+    raw = rng.normal(size=(4, 2 * 50))
+    raw[0, 4:6] = 0.0
+    raw[1, 6:8] = (1e-9, 0.0)
+    g = rng.normal(size=(4, 53, 3))
+    x = ct.torsion_forward(torch.tensor(raw), c.lengths, c.sin, c.cos)
+    xr = o.torsion_forward(raw, c)
+    assert np.abs(x.numpy() - xr).max() <= 1e-12
+    gr = o.torsion_backward(raw, xr, g, c)
+    got = ct.torsion_backward(torch.tensor(raw), x, torch.tensor(g), c.lengths)
+    assert np.abs(got.numpy() - gr).max() <= 1e-10 * np.abs(gr).max()
