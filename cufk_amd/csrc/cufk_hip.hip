@@ -8,6 +8,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <mutex>
 
 #include "launch.h"
 
@@ -58,6 +59,34 @@ inline TorsionArgs torsion_args(const cufk_torsion_consts& c) {
 
 template <typename T> const T* cp(const void* p) { return static_cast<const T*>(p); }
 template <typename T> T* mp(void* p) { return static_cast<T*>(p); }
+
+// ---------------------------------------------------------------------------- static scratch
+
+// Scratch of cufk_reconstruct_bwd_anchored_noalloc: the per-chain force and torque sums that
+// cufk_reconstruct_bwd_anchored keeps in its anchor_work argument, six doubles per chain.  Every
+// GPU the library runs on holds one copy (3 MiB) until the process ends.  In host code the name
+// `scratch` is a stand-in, not a device address: kernels get the address that
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+constexpr int64_t kNoAllocMaxChains = CUFK_NOALLOC_MAX_CHAINS;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) double scratch[6 * kNoAllocMaxChains];
+
+// The device address of `scratch` on the current device, or a status.  The first call on a
+// device looks it up (this allocates nothing; the array is part of the loaded code object).
+inline int scratch_on_current_device(double** out) {
+  static std::mutex mutex;
+  static double* address[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CUFK_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (address[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return CUFK_ERR_DEVICE;
+    address[dev] = static_cast<double*>(p);
+  }
+  *out = address[dev];
+  return CUFK_OK;
+}
 
 }  // namespace cufk_amd
 
@@ -270,6 +299,24 @@ int cufk_reconstruct_bwd_anchored(int dtype, const void* lengths, const void* an
   });
 }
 
+int cufk_reconstruct_bwd_anchored_noalloc(int dtype, const void* lengths, const void* angles,
+                                          const void* dihedrals, const void* p0, const void* first_direction,
+                                          const void* initial_normal, const void* xyz, const uint8_t* chain_regular,
+                                          const void* grad_xyz, void* grad_lengths, void* grad_angles,
+                                          void* grad_dihedrals, void* grad_p0, void* grad_first_direction,
+                                          void* grad_initial_normal, int64_t batch, int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch > kNoAllocMaxChains) return CUFK_ERR_SCRATCH;
+  double* work = nullptr;
+  const int sc = scratch_on_current_device(&work);
+  if (sc != CUFK_OK) return sc;
+  return cufk_reconstruct_bwd_anchored(dtype, lengths, angles, dihedrals, p0, first_direction, initial_normal, xyz,
+                                       chain_regular, grad_xyz, grad_lengths, grad_angles, grad_dihedrals, work,
+                                       grad_p0, grad_first_direction, grad_initial_normal, batch, points, stream);
+}
+
 int cufk_reconstruct_loss_fwd(int dtype, const void* lengths, const void* angles, const void* dihedrals,
                               const void* p0, const void* first_direction, const void* initial_normal,
                               const void* target, void* xyz, uint8_t* chain_regular, void* loss, int64_t batch,
@@ -384,6 +431,7 @@ const char* cufk_error_string(int status) {
     case CUFK_ERR_LAUNCH: return "kernel launch failed";
     case CUFK_ERR_DEVICE: return "device query failed";
     case CUFK_ERR_SEGMENT: return "segment length must be in [1, 2048] local transforms";
+    case CUFK_ERR_SCRATCH: return "batch exceeds the 65536 chains of the allocation-free entry point's static scratch";
     default: return "unknown status";
   }
 }

@@ -41,8 +41,12 @@ enum cufk_status {
   CUFK_ERR_STRIDE = 6,      /* raw-pair row stride shorter than the row */
   CUFK_ERR_LAUNCH = 7,      /* kernel launch failed (C10_CUDA_KERNEL_LAUNCH_CHECK, block.cu:327) */
   CUFK_ERR_DEVICE = 8,      /* device query failed */
-  CUFK_ERR_SEGMENT = 9      /* long-chain segment length outside [1, 2048] */
+  CUFK_ERR_SEGMENT = 9,     /* long-chain segment length outside [1, 2048] */
+  CUFK_ERR_SCRATCH = 10     /* batch larger than the static scratch of an allocation-free entry point */
 };
+
+/* Chains per call of cufk_reconstruct_bwd_anchored_noalloc (its static scratch: 6 doubles each). */
+#define CUFK_NOALLOC_MAX_CHAINS 65536
 
 /* Direction argument of cufk_max_steps. */
 enum cufk_direction { CUFK_FORWARD = 0, CUFK_BACKWARD = 1 };
@@ -168,6 +172,24 @@ int cufk_reconstruct_bwd_anchored(int dtype, const void* lengths, const void* an
                                   void* grad_lengths, void* grad_angles, void* grad_dihedrals, double* anchor_work,
                                   void* grad_p0, void* grad_first_direction, void* grad_initial_normal, int64_t batch,
                                   int64_t points, void* stream);
+
+/*
+ * cufk_reconstruct_bwd_anchored without the anchor_work argument: it allocates nothing and
+ * takes no workspace, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The per-chain sums live in a static device array of the library, one per GPU,
+ * of CUFK_NOALLOC_MAX_CHAINS * 6 doubles (3 MiB, held until the process ends); batch >
+ * CUFK_NOALLOC_MAX_CHAINS returns CUFK_ERR_SCRATCH.  Call it with the stream's device current.
+ * Every call on one GPU shares that array: calls that overlap in time on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller.  Results equal
+ * those of cufk_reconstruct_bwd_anchored.
+ */
+int cufk_reconstruct_bwd_anchored_noalloc(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                          const void* p0, const void* first_direction, const void* initial_normal,
+                                          const void* xyz, const uint8_t* chain_regular, const void* grad_xyz,
+                                          void* grad_lengths, void* grad_angles, void* grad_dihedrals, void* grad_p0,
+                                          void* grad_first_direction, void* grad_initial_normal, int64_t batch,
+                                          int64_t points, void* stream);
 
 /*
  * Fused coordinate loss: loss[b] = sum_i |x_bi - target_bi|^2 over the points of chain b, with

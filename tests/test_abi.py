@@ -28,6 +28,7 @@ def lib():
     lib.cufk_torsion_fwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, i64, i64, vp]
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
     lib.cufk_reconstruct_bwd_anchored.argtypes = [ctypes.c_int] + [vp] * 16 + [i64, i64, vp]
+    lib.cufk_reconstruct_bwd_anchored_noalloc.argtypes = [ctypes.c_int] + [vp] * 15 + [i64, i64, vp]
     lib.cufk_reconstruct_loss_fwd.argtypes = [ctypes.c_int] + [vp] * 10 + [i64, i64, vp]
     lib.cufk_reconstruct_loss_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, vp]
     lib.cufk_reconstruct_long_fwd.argtypes = [ctypes.c_int] + [vp] * 8 + [i64, i64, i64, vp]
@@ -60,6 +61,7 @@ def test_header_declares_the_entry_points():
         "cufk_max_steps",
         "cufk_reconstruct_bwd",
         "cufk_reconstruct_bwd_anchored",
+        "cufk_reconstruct_bwd_anchored_noalloc",
         "cufk_reconstruct_bwd_saved",
         "cufk_reconstruct_bwd_shadow",
         "cufk_reconstruct_fwd",
@@ -227,3 +229,20 @@ def test_anchored_status_paths(lib):
     assert f(0, p, p, p, p, p, p, p, null, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_NULL  # xyz needs its flags
     assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 10, null) == ERR_NULL  # scratch is required
     assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, null, p, p, 4, 10, null) == ERR_NULL  # anchor gradients too
+
+
+ERR_SCRATCH = 10
+
+
+def test_anchored_noalloc_status_paths(lib):
+    """The allocation-free anchored backward checks its arguments before it looks up its static
+    scratch on the device: no GPU is touched by these calls."""
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_bwd_anchored_noalloc
+    #        dtype L  A  D  p0 d0 n0 xyz flags g  gL gA gD gp0 gd0 gn0
+    assert f(9, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 4, 2052, null) == ERR_STEPS
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 65537, 10, null) == ERR_SCRATCH
+    assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 65537, 3, null) == ERR_POINTS
+    assert lib.cufk_error_string(ERR_SCRATCH).startswith(b"batch exceeds the 65536 chains")
