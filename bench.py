@@ -79,9 +79,11 @@ ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 
 # HBM bytes per step (forward + backward launch) from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # each counter scaled by what it reads for a plain copy of known size; the per-kernel figures are
-# in profiles/reconstruct_c2_hbm_traffic.md.  A config without an entry reports traffic as null.
+# in profiles/hbm_traffic_c2_c3_c4.md.  A config without an entry reports traffic as null.
 MEASURED_TRAFFIC = {
-    "c2": 203211803 + 303489063,  # forward (read 102350363, write 100861440) + backward (202659879 + 100829184)
+    "c2": 203296092 + 303465350,  # forward (read 102434140, write 100861952) + backward (202636371 + 100828979)
+    "c3": 126570527 + 254119503,  # torsion forward (50548153 + 76022374) + backward (203780687 + 50338816)
+    "c4_bf16": 409686435 + 408598374,  # forward with the float copy (106083543 + 303602893) + backward (306951629 + 101646746)
 }
 
 
