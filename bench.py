@@ -71,6 +71,12 @@ CONFIGS = {
     # reconstruct_loss (reconstruction fused with a per-chain coordinate loss) at C2's shape; the
     # unfused composition (reconstruct, then the loss in torch) is timed beside it.
     "loss": ("loss", "float32", 4096, 2049),
+    # reconstruct_rmsd (the reconstruction fused with the RMSD after optimal superposition) at
+    # C2's shape, against reconstruct followed by the Kabsch superposition in torch.
+    "rmsd": ("rmsd", "float32", 4096, 2049),
+    # compile_torsion(...).loss (the torsion path fused with a coordinate loss) at C3's shape,
+    # against the torsion path followed by the loss in torch.
+    "torsion_loss": ("torsion_loss", "float32", 8192, 771),
 }
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
@@ -201,13 +207,14 @@ def cpu_baseline(torch, kind, B, N, runs, seconds):
     threads = torch.get_num_threads()  # torch's intra-op pool: OMP_NUM_THREADS or the host's cores
     gen = torch.Generator().manual_seed(1000)
     consts = None
-    if kind == "torsion":
+    torsion = kind in ("torsion", "torsion_loss")
+    if torsion:
         from oracle import nerf64 as o
 
         consts = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
 
     def make(n):
-        if kind == "torsion":
+        if torsion:
             raw = torch.randn(n, 2 * (N - 3), generator=gen, dtype=torch.float64)
             return raw, torch.randn(n, N, 3, generator=gen, dtype=torch.float64)
         L = (torch.randn(n, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
@@ -220,15 +227,28 @@ def cpu_baseline(torch, kind, B, N, runs, seconds):
 
     def run(inputs):
         t0 = time.perf_counter()
-        if kind == "torsion":
+        if torsion:
             raw, g = inputs
             x = ct.torsion_forward(raw, consts.lengths, consts.sin, consts.cos)
+            if kind == "torsion_loss":
+                g = 2.0 * (x - g)  # the coordinate loss against target g
             ct.torsion_backward(raw, x, g, consts.lengths)
         else:
             L, A, D, g, p0, fd, n0 = inputs
             x = ct.forward(L, A, D, p0, fd, n0)
             if kind == "loss":
                 g = 2.0 * (x - g * 0.3)  # the loss against the same target bench.py uses on the GPU
+            elif kind == "rmsd":  # Kabsch by SVD, then the RMSD's grad_xyz
+                t = x + g * 0.3
+                xc, tc = x - x.mean(1, keepdim=True), t - t.mean(1, keepdim=True)
+                U, _, Vh = torch.linalg.svd(xc.transpose(1, 2) @ tc)
+                V, Ut = Vh.transpose(1, 2), U.transpose(1, 2)
+                dsign = torch.sign(torch.linalg.det(V @ Ut))
+                Dm = torch.diag_embed(torch.stack([torch.ones_like(dsign), torch.ones_like(dsign), dsign], -1))
+                Rt = (V @ Dm @ Ut).transpose(1, 2)
+                r = xc @ Rt - tc
+                rmsd = r.pow(2).sum(-1).mean(-1).sqrt()
+                g = (r @ Rt.transpose(1, 2)) / (N * rmsd[:, None, None])
             ct.backward(x, g)
         return time.perf_counter() - t0
 
@@ -355,6 +375,61 @@ def main():
             unfused.append(plain)
             fonly.append(lambda L=L, A=A, D=D, t=target, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct_loss(L, A, D, t, p0,
                                                                                                        fd, n0))
+    elif kind == "rmsd":
+        # As the coordinate loss (s(9N-6) each way) plus a 24-double superposition record per
+        # chain written by the forward and read by the backward.
+        fwd_bytes = s * B * (9 * N - 6) + 8 * 24 * B
+        bwd_bytes = s * B * (9 * N - 6) + 8 * 24 * B
+        unfused = []
+        for k in range(nsets):
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype)
+            with torch.no_grad():
+                target = cufk_amd.reconstruct(L, A, D, p0, fd, n0) + g * 0.3
+            for t in (L, A, D):
+                t.requires_grad_(True)
+
+            def step(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
+                loss = cufk_amd.reconstruct_rmsd(L, A, D, target, p0, fd, n0)
+                return torch.autograd.grad(loss.sum(), (L, A, D))
+
+            def plain(L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0):
+                # Kabsch by SVD of the batched 3x3 cross-covariances; the rotation is held fixed in
+                # the backward (its own dependence drops out at the optimum).
+                x = cufk_amd.reconstruct(L, A, D, p0, fd, n0)
+                xc, tc = x - x.mean(1, keepdim=True), target - target.mean(1, keepdim=True)
+                U, _, Vh = torch.linalg.svd((xc.transpose(1, 2) @ tc).detach())
+                V, Ut = Vh.transpose(1, 2), U.transpose(1, 2)
+                dsign = torch.sign(torch.linalg.det(V @ Ut))
+                Dm = torch.diag_embed(torch.stack([torch.ones_like(dsign), torch.ones_like(dsign), dsign], -1))
+                Rt = (V @ Dm @ Ut).transpose(1, 2).contiguous()
+                rmsd = ((xc @ Rt - tc) ** 2).sum(-1).mean(-1).sqrt()
+                return torch.autograd.grad(rmsd.sum(), (L, A, D))
+
+            loss_out = torch.empty(B, device=device, dtype=dtype)
+            xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+            flags = torch.empty(B, device=device, dtype=torch.uint8)
+            rec = torch.empty(B, 24, device=device, dtype=torch.float64)
+            gL, gA, gD = torch.empty_like(L), torch.empty_like(A), torch.empty_like(D)
+
+            def fwd(st, L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, loss_out=loss_out,
+                    rec=rec):
+                rc = lib.cufk_reconstruct_superposed_fwd(code, 2, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(target),
+                                                         P(xyz), P(flags), P(loss_out), P(rec), i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            def bwd(st, L=L, A=A, D=D, target=target, p0=p0, fd=fd, n0=n0, xyz=xyz, flags=flags, rec=rec, gL=gL,
+                    gA=gA, gD=gD):
+                rc = lib.cufk_reconstruct_superposed_bwd(code, 2, P(L), P(A), P(D), P(p0), P(fd), P(n0), P(xyz),
+                                                         P(flags), P(target), P(rec), None, P(gL), P(gA), P(gD),
+                                                         i64(B), i64(N), st)
+                assert rc == 0, rc
+
+            steps.append(step)
+            fwds.append(fwd)
+            bwds.append(bwd)
+            unfused.append(plain)
+            fonly.append(lambda L=L, A=A, D=D, t=target, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct_rmsd(L, A, D, t, p0,
+                                                                                                       fd, n0))
     elif kind == "reconstruct":
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
@@ -414,34 +489,58 @@ def main():
         c = Consts((ctypes.c_float * 3)(*BOND_LENGTHS), (ctypes.c_double * 3)(*[math.sin(a) for a in BOND_ANGLES]),
                    (ctypes.c_double * 3)(*[math.cos(a) for a in BOND_ANGLES]))
         f = cufk_amd.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
-        fwd_bytes = s * B * (5 * N - 6)
+        fused = kind == "torsion_loss"
+        # Torsion: forward s(5N-6), backward s(10N-12).  With the fused coordinate loss the
+        # forward also reads the target (3N) and the backward reads the target in place of
+        # grad_xyz (same count).
+        fwd_bytes = s * B * (5 * N - 6 + (3 * N if fused else 0))
         bwd_bytes = s * B * (10 * N - 12)
+        unfused = []
         for k in range(nsets):
             gen = torch.Generator().manual_seed(3 + k)
             raw = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
             g = torch.randn(B, N, 3, generator=gen, dtype=torch.float64).to(device=device, dtype=dtype)
             raw.requires_grad_(True)
 
-            def step(raw=raw, g=g):
-                xyz = f(raw)
-                return torch.autograd.grad(xyz, (raw,), g)
+            if fused:
+                def step(raw=raw, target=g):
+                    return torch.autograd.grad(f.loss(raw, target).sum(), (raw,))
+
+                def plain(raw=raw, target=g):
+                    return torch.autograd.grad(((f(raw) - target) ** 2).sum(), (raw,))
+
+                unfused.append(plain)
+            else:
+                def step(raw=raw, g=g):
+                    xyz = f(raw)
+                    return torch.autograd.grad(xyz, (raw,), g)
 
             xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
             graw = torch.empty_like(raw)
+            loss_out = torch.empty(B, device=device, dtype=dtype)
 
-            def fwd(st, raw=raw, xyz=xyz):
-                rc = lib.cufk_torsion_fwd(code, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(xyz), i64(B), i64(N), st)
+            def fwd(st, raw=raw, xyz=xyz, target=g, loss_out=loss_out):
+                if fused:
+                    rc = lib.cufk_torsion_loss_fwd(code, 0, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(target),
+                                                   P(xyz), P(loss_out), None, i64(B), i64(N), st)
+                else:
+                    rc = lib.cufk_torsion_fwd(code, P(raw), i64(raw.stride(0)), ctypes.byref(c), P(xyz), i64(B), i64(N),
+                                              st)
                 assert rc == 0, rc
 
             def bwd(st, raw=raw, xyz=xyz, g=g, graw=graw):
-                rc = lib.cufk_torsion_bwd(code, P(raw), i64(raw.stride(0)), P(xyz), P(g), P(graw), i64(graw.stride(0)),
-                                          ctypes.byref(c), i64(B), i64(N), st)
+                if fused:
+                    rc = lib.cufk_torsion_loss_bwd(code, 0, P(raw), i64(raw.stride(0)), P(xyz), P(g), None, None,
+                                                   P(graw), i64(graw.stride(0)), ctypes.byref(c), i64(B), i64(N), st)
+                else:
+                    rc = lib.cufk_torsion_bwd(code, P(raw), i64(raw.stride(0)), P(xyz), P(g), P(graw),
+                                              i64(graw.stride(0)), ctypes.byref(c), i64(B), i64(N), st)
                 assert rc == 0, rc
 
             steps.append(step)
             fwds.append(fwd)
             bwds.append(bwd)
-            fonly.append(lambda raw=raw: f(raw))
+            fonly.append((lambda raw=raw, target=g: f.loss(raw, target)) if fused else (lambda raw=raw: f(raw)))
 
     if args.graph:
         # One graph per input set: warm up on a side stream, capture, then the timed steps
@@ -518,7 +617,7 @@ def main():
     regular_frac = float(torch.stack(regular).float().mean()) if regular else None
 
     unfused_us = None
-    if kind == "loss":  # the same step through reconstruct and a torch loss, same input sets
+    if kind in ("loss", "rmsd", "torsion_loss"):  # the same step unfused (the loss in torch), same input sets
         for i in range(args.warmup):
             unfused[i % nsets]()
         torch.cuda.synchronize()

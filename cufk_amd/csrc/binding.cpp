@@ -379,6 +379,78 @@ Tensor apply_loss(const Tensor& lengths, const Tensor& angles, const Tensor& dih
   return LossAutograd::apply(lengths, angles, dihedrals, target, p0, first_direction, initial_normal);
 }
 
+// ------------------------------------------------------------------ fused superposed loss
+
+// loss[b] = mean squared deviation of the reconstruction from target[b] after optimal
+// superposition (kind CUFK_LOSS_MSD), or its square root (CUFK_LOSS_RMSD); no reference
+// counterpart.  Gradients flow to lengths, angles and dihedrals.
+class SuperposedAutograd : public torch::autograd::Function<SuperposedAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
+                        Tensor target, Tensor p0, Tensor first_direction, Tensor initial_normal, int64_t kind) {
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    check_like(target, lengths, "target", true);
+    TORCH_CHECK(target.sizes() == torch::IntArrayRef({shape.batch, shape.points, 3}), "target must have shape (B, N, 3)");
+    TORCH_CHECK(!target.requires_grad(), "target gradients are not supported");
+    const c10::DeviceGuard guard(lengths.device());
+    check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
+    Tensor loss = torch::empty({shape.batch}, lengths.options());
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
+    Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
+    Tensor record = torch::empty({shape.batch, CUFK_SUPERPOSITION_DOUBLES}, lengths.options().dtype(torch::kFloat64));
+    check_status(cufk_reconstruct_superposed_fwd(dtype_code(lengths), static_cast<int>(kind), lengths.data_ptr(),
+                                                 angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(),
+                                                 a.first_direction.data_ptr(), a.initial_normal.data_ptr(),
+                                                 target.data_ptr(), xyz.data_ptr(),
+                                                 static_cast<uint8_t*>(regular.data_ptr()), loss.data_ptr(),
+                                                 static_cast<double*>(record.data_ptr()), shape.batch, shape.points,
+                                                 current_stream(lengths)),
+                 "cufk_reconstruct_superposed_fwd");
+    ctx->save_for_backward({lengths, angles, dihedrals, target, a.p0, a.first_direction, a.initial_normal});
+    ctx->saved_data["xyz"] = xyz;
+    ctx->saved_data["regular"] = regular;
+    ctx->saved_data["record"] = record;
+    ctx->saved_data["kind"] = kind;
+    return loss;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& lengths = saved[0];
+    const Tensor& angles = saved[1];
+    const Tensor& dihedrals = saved[2];
+    const Tensor& target = saved[3];
+    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true);
+    Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_loss, lengths, "grad_loss", true);
+    const c10::DeviceGuard guard(lengths.device());
+    Tensor grad_lengths = torch::empty_like(lengths);
+    Tensor grad_angles = torch::empty_like(angles);
+    Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    const Tensor regular = ctx->saved_data["regular"].toTensor();
+    const Tensor record = ctx->saved_data["record"].toTensor();
+    check_status(cufk_reconstruct_superposed_bwd(
+                     dtype_code(lengths), static_cast<int>(ctx->saved_data["kind"].toInt()), lengths.data_ptr(),
+                     angles.data_ptr(), dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
+                     a.initial_normal.data_ptr(), xyz.data_ptr(), static_cast<const uint8_t*>(regular.data_ptr()),
+                     target.data_ptr(), static_cast<const double*>(record.data_ptr()), grad_loss.data_ptr(),
+                     grad_lengths.data_ptr(), grad_angles.data_ptr(), grad_dihedrals.data_ptr(), shape.batch,
+                     shape.points, current_stream(lengths)),
+                 "cufk_reconstruct_superposed_bwd");
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+  }
+};
+
+Tensor apply_superposed(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& target,
+                        const Tensor& p0, const Tensor& first_direction, const Tensor& initial_normal, int64_t kind) {
+  TORCH_CHECK(kind == CUFK_LOSS_MSD || kind == CUFK_LOSS_RMSD, "unknown superposed loss kind ", kind);
+  return SuperposedAutograd::apply(lengths, angles, dihedrals, target, p0, first_direction, initial_normal, kind);
+}
+
 // ------------------------------------------------------------------ long chains
 
 // Segmented reconstruction without the 2048-step cap (no reference counterpart: its README:58
@@ -517,6 +589,63 @@ class TorsionAutograd : public torch::autograd::Function<TorsionAutograd> {
   }
 };
 
+// The torsion path with a fused loss against target (any cufk_loss kind; no reference
+// counterpart): the reference's backward (torsion.cu:297-381) consumes a materialised
+// grad_xyz, which here is formed inside the kernel from the saved positions and the target.
+class TorsionLossAutograd : public torch::autograd::Function<TorsionLossAutograd> {
+ public:
+  static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor raw_pairs, Tensor target,
+                        std::vector<double> packed, int64_t kind) {
+    const Shape shape = check_pairs(raw_pairs, true);
+    check_like(target, raw_pairs, "target", true);
+    TORCH_CHECK(target.sizes() == torch::IntArrayRef({shape.batch, shape.points, 3}), "target must have shape (B, N, 3)");
+    TORCH_CHECK(!target.requires_grad(), "target gradients are not supported");
+    const c10::DeviceGuard guard(raw_pairs.device());
+    check_max_local_transforms(shape.points - 3, max_steps(raw_pairs, CUFK_FORWARD), "torsion_pairs");
+    const cufk_torsion_consts c = consts_from(packed);
+    Tensor xyz = torch::empty({shape.batch, shape.points, 3}, raw_pairs.options());
+    Tensor loss = torch::empty({shape.batch}, raw_pairs.options());
+    Tensor record = kind == CUFK_LOSS_SQUARED_DISTANCE
+                        ? Tensor()
+                        : torch::empty({shape.batch, CUFK_SUPERPOSITION_DOUBLES}, raw_pairs.options().dtype(torch::kFloat64));
+    double* rec = record.defined() ? static_cast<double*>(record.data_ptr()) : nullptr;
+    check_status(cufk_torsion_loss_fwd(dtype_code(raw_pairs), static_cast<int>(kind), raw_pairs.data_ptr(),
+                                       raw_pairs.stride(0), &c, target.data_ptr(), xyz.data_ptr(), loss.data_ptr(), rec,
+                                       shape.batch, shape.points, current_stream(raw_pairs)),
+                 "cufk_torsion_loss_fwd");
+    ctx->save_for_backward({raw_pairs, target});
+    ctx->saved_data["xyz"] = xyz;
+    if (record.defined()) ctx->saved_data["record"] = record;
+    ctx->saved_data["consts"] = c10::List<double>(packed);
+    ctx->saved_data["kind"] = kind;
+    return loss;
+  }
+
+  static torch::autograd::tensor_list backward(torch::autograd::AutogradContext* ctx,
+                                               torch::autograd::tensor_list grad_outputs) {
+    const auto saved = ctx->get_saved_variables();
+    const Tensor& raw_pairs = saved[0];
+    const Tensor& target = saved[1];
+    Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
+    check_like(grad_loss, raw_pairs, "grad_loss", true);
+    const Shape shape = check_pairs(raw_pairs, true);
+    const c10::DeviceGuard guard(raw_pairs.device());
+    const auto list = ctx->saved_data["consts"].toDoubleList();
+    const cufk_torsion_consts c = consts_from(std::vector<double>(list.begin(), list.end()));
+    const int kind = static_cast<int>(ctx->saved_data["kind"].toInt());
+    const Tensor xyz = ctx->saved_data["xyz"].toTensor();
+    const double* rec = nullptr;
+    if (kind != CUFK_LOSS_SQUARED_DISTANCE) rec = static_cast<const double*>(ctx->saved_data["record"].toTensor().data_ptr());
+    // extension_utils.cuh:162-164: the gradient keeps the raw tensor's strides.
+    Tensor grad = torch::empty_strided(raw_pairs.sizes(), raw_pairs.strides(), raw_pairs.options());
+    check_status(cufk_torsion_loss_bwd(dtype_code(raw_pairs), kind, raw_pairs.data_ptr(), raw_pairs.stride(0),
+                                       xyz.data_ptr(), target.data_ptr(), rec, grad_loss.data_ptr(), grad.data_ptr(),
+                                       grad.stride(0), &c, shape.batch, shape.points, current_stream(raw_pairs)),
+                 "cufk_torsion_loss_bwd");
+    return {grad, Tensor(), Tensor(), Tensor()};
+  }
+};
+
 // A compiled torsion reconstructor: the three bond lengths and bond-angle sin/cos fixed at
 // construction (torsion.py:89-135 compiles them into a JIT module instead).
 class TorsionModule {
@@ -529,6 +658,10 @@ class TorsionModule {
     for (double v : coss) packed_.push_back(v);
   }
   Tensor apply(const Tensor& raw_pairs) const { return TorsionAutograd::apply(raw_pairs, packed_); }
+  Tensor loss(const Tensor& raw_pairs, const Tensor& target, int64_t kind) const {
+    TORCH_CHECK(kind >= CUFK_LOSS_SQUARED_DISTANCE && kind <= CUFK_LOSS_RMSD, "unknown loss kind ", kind);
+    return TorsionLossAutograd::apply(raw_pairs, target, packed_, kind);
+  }
   std::vector<double> lengths() const { return {packed_[0], packed_[1], packed_[2]}; }
   std::vector<double> sins() const { return {packed_[3], packed_[4], packed_[5]}; }
   std::vector<double> coss() const { return {packed_[6], packed_[7], packed_[8]}; }
@@ -568,6 +701,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("apply_loss", &apply_loss, "fused reconstruct + per-chain coordinate loss", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"), py::arg("first_direction"),
         py::arg("initial_normal"));
+  m.def("apply_superposed", &apply_superposed, "fused reconstruct + per-chain superposed loss (1 msd, 2 rmsd)",
+        py::arg("lengths"), py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"),
+        py::arg("first_direction"), py::arg("initial_normal"), py::arg("kind"));
   m.def("apply_long", &apply_reconstruct_long, "segmented reconstruct for chains of any length", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"),
         py::arg("segment_steps") = 0);
@@ -577,6 +713,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            py::arg("lengths"), py::arg("sin"), py::arg("cos"))
       .def("apply", &TorsionModule::apply, "torsion-only autograd apply (torsion.cu:445-447)", py::arg("raw_pairs"))
       .def("__call__", &TorsionModule::apply, py::arg("raw_pairs"))
+      .def("loss", &TorsionModule::loss, "torsion path with a fused loss (0 squared distance, 1 msd, 2 rmsd)",
+           py::arg("raw_pairs"), py::arg("target"), py::arg("kind"))
       .def_property_readonly("lengths", &TorsionModule::lengths)
       .def_property_readonly("sin", &TorsionModule::sins)
       .def_property_readonly("cos", &TorsionModule::coss);

@@ -357,6 +357,95 @@ int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles
   });
 }
 
+int cufk_reconstruct_superposed_fwd(int dtype, int loss_kind, const void* lengths, const void* angles,
+                                    const void* dihedrals, const void* p0, const void* first_direction,
+                                    const void* initial_normal, const void* target, void* xyz, uint8_t* chain_regular,
+                                    void* loss, double* superposition, int64_t batch, int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  if (loss_kind != CUFK_LOSS_MSD && loss_kind != CUFK_LOSS_RMSD) return CUFK_ERR_LOSS;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !target || !xyz ||
+      !chain_regular || !loss || !superposition)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  const int squared = loss_kind == CUFK_LOSS_MSD;
+  return dispatch(dtype, [&]<typename T>() {
+    return superposed_fwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                                   cp<T>(initial_normal), cp<T>(target), mp<T>(xyz), chain_regular, mp<T>(loss),
+                                   superposition, squared, batch, static_cast<int>(points), st);
+  });
+}
+
+int cufk_reconstruct_superposed_bwd(int dtype, int loss_kind, const void* lengths, const void* angles,
+                                    const void* dihedrals, const void* p0, const void* first_direction,
+                                    const void* initial_normal, const void* xyz, const uint8_t* chain_regular,
+                                    const void* target, const double* superposition, const void* grad_loss,
+                                    void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                                    int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  if (loss_kind != CUFK_LOSS_MSD && loss_kind != CUFK_LOSS_RMSD) return CUFK_ERR_LOSS;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (batch == 0) return CUFK_OK;
+  if (!lengths || !angles || !dihedrals || !p0 || !first_direction || !initial_normal || !xyz || !chain_regular ||
+      !target || !superposition || !grad_lengths || !grad_angles || !grad_dihedrals)
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  const int squared = loss_kind == CUFK_LOSS_MSD;
+  return dispatch(dtype, [&]<typename T>() {
+    return superposed_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0), cp<T>(first_direction),
+                                   cp<T>(initial_normal), cp<T>(xyz), chain_regular, cp<T>(target), superposition,
+                                   cp<T>(grad_loss), squared, mp<T>(grad_lengths), mp<T>(grad_angles),
+                                   mp<T>(grad_dihedrals), batch, static_cast<int>(points), st);
+  });
+}
+
+int cufk_torsion_loss_fwd(int dtype, int loss_kind, const void* raw_pairs, int64_t raw_stride,
+                          const cufk_torsion_consts* consts, const void* target, void* xyz, void* loss,
+                          double* superposition, int64_t batch, int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  if (loss_kind < CUFK_LOSS_SQUARED_DISTANCE || loss_kind > CUFK_LOSS_RMSD) return CUFK_ERR_LOSS;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (raw_stride < 0) return CUFK_ERR_STRIDE;
+  if (!consts) return CUFK_ERR_NULL;
+  if (batch == 0) return CUFK_OK;
+  const bool superposed = loss_kind != CUFK_LOSS_SQUARED_DISTANCE;
+  if (!raw_pairs || !target || !xyz || !loss || (superposed && !superposition)) return CUFK_ERR_NULL;
+  const TorsionArgs args = torsion_args(*consts);
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return torsion_loss_fwd_typed<T>(superposed ? kLossSuperposed : kLossSquared, cp<T>(raw_pairs), raw_stride, args,
+                                     cp<T>(target), mp<T>(xyz), mp<T>(loss), superposed ? superposition : nullptr,
+                                     loss_kind == CUFK_LOSS_MSD, batch, static_cast<int>(points), st);
+  });
+}
+
+int cufk_torsion_loss_bwd(int dtype, int loss_kind, const void* raw_pairs, int64_t raw_stride, const void* xyz,
+                          const void* target, const double* superposition, const void* grad_loss, void* grad_raw,
+                          int64_t grad_raw_stride, const cufk_torsion_consts* consts, int64_t batch, int64_t points,
+                          void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  if (loss_kind < CUFK_LOSS_SQUARED_DISTANCE || loss_kind > CUFK_LOSS_RMSD) return CUFK_ERR_LOSS;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (raw_stride < 0 || grad_raw_stride < 0) return CUFK_ERR_STRIDE;
+  if (!consts) return CUFK_ERR_NULL;
+  if (batch == 0) return CUFK_OK;
+  const bool superposed = loss_kind != CUFK_LOSS_SQUARED_DISTANCE;
+  if (!raw_pairs || !xyz || !target || !grad_raw || (superposed && !superposition)) return CUFK_ERR_NULL;
+  const TorsionArgs args = torsion_args(*consts);
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    return torsion_loss_bwd_typed<T>(superposed ? kLossSuperposed : kLossSquared, cp<T>(raw_pairs), raw_stride,
+                                     cp<T>(xyz), cp<T>(target), superposed ? superposition : nullptr,
+                                     cp<T>(grad_loss), loss_kind == CUFK_LOSS_MSD, mp<T>(grad_raw), grad_raw_stride,
+                                     args, batch, static_cast<int>(points), st);
+  });
+}
+
 int64_t cufk_long_segment_steps(int64_t batch, int64_t points) {
   if (batch < 0 || points < 4) return 0;
   int64_t S = kMaxSteps;
@@ -432,6 +521,7 @@ const char* cufk_error_string(int status) {
     case CUFK_ERR_DEVICE: return "device query failed";
     case CUFK_ERR_SEGMENT: return "segment length must be in [1, 2048] local transforms";
     case CUFK_ERR_SCRATCH: return "batch exceeds the 65536 chains of the allocation-free entry point's static scratch";
+    case CUFK_ERR_LOSS: return "unknown or unsupported loss kind";
     default: return "unknown status";
   }
 }

@@ -1,0 +1,165 @@
+// Pieces of the fused losses shared by the reconstruct and torsion kernels.
+//
+// No reference counterpart: the reference returns coordinates and leaves the loss to PyTorch.
+// A fused loss reduces a per-chain loss from the positions in registers in the forward, and
+// forms grad_xyz from the saved positions and the target inside the backward, so neither the
+// loss terms nor grad_xyz ever exist in HBM.
+//   kLossSquared     sum_i |x_i - t_i|^2
+//   kLossSuperposed  mean squared deviation after optimal superposition (superpose.h), or its
+//                    square root (the RMSD)
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "chain_ops.h"
+#include "superpose.h"
+
+namespace cufk_amd {
+
+constexpr int kLossNone = 0;
+constexpr int kLossSquared = 1;
+constexpr int kLossSuperposed = 2;
+
+// Gradient of a fused loss with respect to one point x (target t), formed inside the backward.
+struct NoResidual {};
+// sum_i |x_i - t_i|^2, times the upstream weight: w2 = 2 w.
+template <typename R> struct SquaredResidual {
+  R w2;
+  __device__ __forceinline__ V3<R> operator()(V3<R> x, V3<R> t) const { return w2 * (x - t); }
+};
+// The superposed losses: c (x - M t - a) with M = R^T and a = xbar - R^T tbar of the chain's
+// optimal superposition, c = (2/N) w for the mean squared deviation (times 1 / (2 rmsd) for
+// the RMSD).  Formed in double and rounded once: x, M t and a are each about the chain's
+// distance from the origin while the residual is a fraction of a nanometre, and M rounded to
+// float would rotate every residual by the same 1e-7 error, which the adjoint's moment sums
+// add up along the chain (measured: 9e-5 relative gradient error at N = 2049 against 1e-5
+// with the residual in double).
+template <typename R> struct SuperposedResidual {
+  double c;
+  double m[9];
+  double a[3];
+  __device__ __forceinline__ V3<R> operator()(V3<R> x, V3<R> t) const {
+    const double tx = t.x, ty = t.y, tz = t.z;
+    const double gx = c * ((static_cast<double>(x.x) - a[0]) - (m[0] * tx + m[1] * ty + m[2] * tz));
+    const double gy = c * ((static_cast<double>(x.y) - a[1]) - (m[3] * tx + m[4] * ty + m[5] * tz));
+    const double gz = c * ((static_cast<double>(x.z) - a[2]) - (m[6] * tx + m[7] * ty + m[8] * tz));
+    return {static_cast<R>(gx), static_cast<R>(gy), static_cast<R>(gz)};
+  }
+};
+
+// The residual of chain `row` for the loss backward: upstream weight w (grad_loss, or 1).
+template <int LossKind, typename R>
+__device__ __forceinline__ auto make_residual(R w, const double* __restrict__ record, int points, int squared) {
+  if constexpr (LossKind == kLossSuperposed) {
+    SuperposedResidual<R> res;
+    const double msd = record[12];
+    double c = 2.0 * static_cast<double>(w) / points;
+    if (!squared) c = msd > 0.0 ? c / (2.0 * sqrt(msd)) : 0.0;
+    res.c = c;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) res.m[k] = record[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) res.a[k] = record[9 + k];
+    return res;
+  } else {
+    return SquaredResidual<R>{R(2) * w};
+  }
+}
+
+// Per-thread accumulation of a chain's loss from its stored positions xs (rounded to the
+// storage type, in the compute type R) and the target t.  The superposed sums are taken about
+// the shift points cx (the chain's stored x2) and ct (the target's point 2), per thread in R
+// over its at most 12 points (float32: about 1e-7 relative of a few products, which leaves the
+// superposed msd good to about 1e-6 relative at N = 2049), then in double across threads.
+template <int LossKind, typename R> struct LossAccumulator {
+  double acc = 0.0;
+  R sp[LossKind == kLossSuperposed ? kSuperposeSums : 1] = {};
+  V3<R> cx = {R(0), R(0), R(0)}, ct = {R(0), R(0), R(0)};
+
+  __device__ __forceinline__ void add(V3<R> xs, V3<R> t) {
+    if constexpr (LossKind == kLossSuperposed) {
+      const V3<R> xd = xs - cx, td = t - ct;
+      const R a[3] = {xd.x, xd.y, xd.z}, b[3] = {td.x, td.y, td.z};
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        sp[i] += a[i];
+        sp[3 + i] += b[i];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) sp[6 + 3 * i + j] += a[i] * b[j];
+      }
+      sp[15] += dot(xd, xd);
+      sp[16] += dot(td, td);
+    } else {
+      const V3<R> d = xs - t;
+      acc += static_cast<double>(dot(d, d));
+    }
+  }
+
+  // Workgroup reduction (W waves; contains one __syncthreads), written by thread 0: the sum of
+  // squares as the chain's loss, or the superposed sums and shift points into the chain's
+  // record, which superpose_records_kernel then solves (it also writes the loss).
+  template <typename T, int W>
+  __device__ __forceinline__ void finish(T* __restrict__ loss, double* __restrict__ record, int lane, int wave,
+                                         int tid) {
+    if constexpr (LossKind == kLossSuperposed) {
+      __shared__ double part[W][kSuperposeSums];
+#pragma unroll
+      for (int k = 0; k < kSuperposeSums; ++k) {
+        const double v = wave_sum(static_cast<double>(sp[k]));
+        if (lane == 0) part[wave][k] = v;
+      }
+      __syncthreads();
+      if (tid < kSuperposeSums) {
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) sum += part[w][tid];
+        record[tid] = sum;
+      } else if (tid < kSuperposeSums + 6) {
+        const int k = tid - kSuperposeSums;
+        const V3<R> c = k < 3 ? cx : ct;
+        record[tid] = static_cast<double>(k % 3 == 0 ? c.x : (k % 3 == 1 ? c.y : c.z));
+      }
+    } else {
+      __shared__ double part[W];
+      const double v = wave_sum(acc);
+      if (lane == 0) part[wave] = v;
+      __syncthreads();
+      if (tid == 0) {
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) sum += part[w];
+        *loss = narrow<T>(static_cast<R>(sum));
+      }
+    }
+  }
+};
+
+}  // namespace cufk_amd
+
+namespace cufk_amd {
+
+// One thread per chain: solve the superposition from the sums the fused forward stored in the
+// chain's record (superpose.h), replace them with the record the backward reads, and write the
+// loss: the mean squared deviation, or its square root unless `squared`.  A separate launch keeps
+// the 4x4 eigenproblem, a serial chain of double operations, out of the forward's workgroups.
+constexpr int kSolveThreads = 256;
+template <typename T>
+__global__ __launch_bounds__(kSolveThreads) void superpose_records_kernel(double* __restrict__ record,
+                                                                          T* __restrict__ loss, int64_t batch,
+                                                                          int points, int squared) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * kSolveThreads + threadIdx.x;
+  if (b >= batch) return;
+  double rec[kSuperposeRecord];
+  double* const r = record + b * kSuperposeRecord;
+#pragma unroll
+  for (int k = 0; k < kSuperposeRecord; ++k) rec[k] = r[k];
+  superpose_solve_record(rec, points);
+#pragma unroll
+  for (int k = 0; k < kSuperposeRecord; ++k) r[k] = rec[k];
+  using R = compute_t<T>;
+  loss[b] = narrow<T>(static_cast<R>(squared ? rec[12] : sqrt(rec[12])));
+}
+
+}  // namespace cufk_amd

@@ -13,6 +13,8 @@
 
 #include "cufk_hip.h"
 #include "reconstruct_kernels.h"  // FastPath
+#include "fused_loss.h"           // kLoss*
+#include "superpose.h"            // kSuperposeRecord
 #include "torsion_kernels.h"      // TorsionArgs
 
 namespace cufk_amd {
@@ -109,6 +111,17 @@ int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
                    const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
                    hipStream_t st);
 
+// Fused superposed losses (mean squared deviation after optimal superposition, or its
+// square root unless `squared`); record: kSuperposeRecord doubles per chain (superpose.h).
+template <typename T>
+int superposed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target,
+                         T* xyz, uint8_t* regular, T* loss, double* record, int squared, int64_t B, int N,
+                         hipStream_t st);
+template <typename T>
+int superposed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                         const uint8_t* regular, const T* target, const double* record, const T* grad_loss,
+                         int squared, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st);
+
 // Chains past the single-workgroup cap, in segments of S steps.
 template <typename T>
 int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, double* state,
@@ -124,5 +137,15 @@ int torsion_fwd_typed(const T* raw, int64_t rs, const TorsionArgs& c, T* xyz, in
 template <typename T>
 int torsion_bwd_typed(const T* raw, int64_t rs, const T* xyz, const T* g, T* graw, int64_t gs, const TorsionArgs& c,
                       int64_t B, int N, hipStream_t st);
+
+// Torsion path with a fused loss (kind: kLossSquared or kLossSuperposed, fused_loss.h); the
+// backward takes the target in place of grad_xyz.
+template <typename T>
+int torsion_loss_fwd_typed(int kind, const T* raw, int64_t rs, const TorsionArgs& c, const T* target, T* xyz, T* loss,
+                           double* record, int squared, int64_t B, int N, hipStream_t st);
+template <typename T>
+int torsion_loss_bwd_typed(int kind, const T* raw, int64_t rs, const T* xyz, const T* target, const double* record,
+                           const T* grad_loss, int squared, T* graw, int64_t gs, const TorsionArgs& c, int64_t B, int N,
+                           hipStream_t st);
 
 }  // namespace cufk_amd

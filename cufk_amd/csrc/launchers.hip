@@ -124,6 +124,19 @@ template <typename Fn> int launch_packed(int64_t B, int C, Fn&& fn) {
   return CUFK_OK;
 }
 
+// The superposed losses' second launch: one thread per chain solves its record.
+template <typename T> int solve_records(double* record, T* loss, int64_t B, int N, int squared, hipStream_t st) {
+  const int64_t groups = (B + kSolveThreads - 1) / kSolveThreads;
+  for (int64_t done = 0; done < groups; done += INT32_MAX) {
+    const int64_t g = groups - done < INT32_MAX ? groups - done : INT32_MAX;
+    const int64_t off = done * kSolveThreads;
+    hipLaunchKernelGGL(superpose_records_kernel<T>, dim3(static_cast<unsigned>(g)), dim3(kSolveThreads), 0, st,
+                       record + off * kSuperposeRecord, loss + off, B - off, N, squared);
+    if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
+  }
+  return CUFK_OK;
+}
+
 }  // namespace cufk_amd
 
 #if CUFK_FAMILY == CUFK_FAMILY_FORWARD
@@ -310,8 +323,40 @@ int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
   });
 }
 
+template <typename T>
+int superposed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target,
+                         T* xyz, uint8_t* regular, T* loss, double* record, int squared, int64_t B, int N,
+                         hipStream_t st) {
+  const int rc = with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_superposed_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+                         L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, target + off * N * 3,
+                         xyz + off * N * 3, regular + off, record + off * kSuperposeRecord, N);
+    });
+  });
+  if (rc != CUFK_OK) return rc;
+  return solve_records<T>(record, loss, B, N, squared, st);
+}
+
+template <typename T>
+int superposed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
+                         const uint8_t* regular, const T* target, const double* record, const T* grad_loss,
+                         int squared, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
+  return with_scan_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad, kLossSuperposed>), dim3(n), dim3(64 * W),
+                         0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
+                         regular + off, target + off * N * 3, grad_loss != nullptr ? grad_loss + off : nullptr,
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
+                         record + off * kSuperposeRecord, squared);
+    });
+  });
+}
+
 CUFK_INSTANTIATE(loss_fwd_typed<CUFK_T>)
 CUFK_INSTANTIATE(loss_bwd_typed<CUFK_T>)
+CUFK_INSTANTIATE(superposed_fwd_typed<CUFK_T>)
+CUFK_INSTANTIATE(superposed_bwd_typed<CUFK_T>)
 
 }  // namespace cufk_amd
 #endif
@@ -393,8 +438,47 @@ int torsion_bwd_typed(const T* raw, int64_t rs, const T* xyz, const T* g, T* gra
   });
 }
 
+template <typename T>
+int torsion_loss_fwd_typed(int kind, const T* raw, int64_t rs, const TorsionArgs& c, const T* target, T* xyz, T* loss,
+                           double* record, int squared, int64_t B, int N, hipStream_t st) {
+  const int rc = with_torsion_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      double* rec = record != nullptr ? record + off * kSuperposeRecord : nullptr;
+      if (kind == kLossSuperposed)
+        hipLaunchKernelGGL((torsion_forward_kernel<T, W, K, kLossSuperposed>), dim3(n), dim3(64 * W), 0, st,
+                           raw + off * rs, rs, c, xyz + off * N * 3, N, target + off * N * 3, nullptr, rec);
+      else
+        hipLaunchKernelGGL((torsion_forward_kernel<T, W, K, kLossSquared>), dim3(n), dim3(64 * W), 0, st, raw + off * rs,
+                           rs, c, xyz + off * N * 3, N, target + off * N * 3, loss + off, nullptr);
+    });
+  });
+  if (rc != CUFK_OK || kind != kLossSuperposed) return rc;
+  return solve_records<T>(record, loss, B, N, squared, st);
+}
+
+template <typename T>
+int torsion_loss_bwd_typed(int kind, const T* raw, int64_t rs, const T* xyz, const T* target, const double* record,
+                           const T* grad_loss, int squared, T* graw, int64_t gs, const TorsionArgs& c, int64_t B, int N,
+                           hipStream_t st) {
+  return with_torsion_bwd_plan(N - 3, [&]<int W, int K>() {
+    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
+      const T* gl = grad_loss != nullptr ? grad_loss + off : nullptr;
+      if (kind == kLossSuperposed)
+        hipLaunchKernelGGL((torsion_backward_kernel<T, W, K, kLossSuperposed>), dim3(n), dim3(64 * W), 0, st,
+                           raw + off * rs, rs, xyz + off * N * 3, target + off * N * 3, graw + off * gs, gs, c, N, gl,
+                           record + off * kSuperposeRecord, squared);
+      else
+        hipLaunchKernelGGL((torsion_backward_kernel<T, W, K, kLossSquared>), dim3(n), dim3(64 * W), 0, st,
+                           raw + off * rs, rs, xyz + off * N * 3, target + off * N * 3, graw + off * gs, gs, c, N, gl,
+                           nullptr, 0);
+    });
+  });
+}
+
 CUFK_INSTANTIATE(torsion_fwd_typed<CUFK_T>)
 CUFK_INSTANTIATE(torsion_bwd_typed<CUFK_T>)
+CUFK_INSTANTIATE(torsion_loss_fwd_typed<CUFK_T>)
+CUFK_INSTANTIATE(torsion_loss_bwd_typed<CUFK_T>)
 
 }  // namespace cufk_amd
 #endif

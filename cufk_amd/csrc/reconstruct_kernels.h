@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "chain_ops.h"
+#include "fused_loss.h"
 #include "staging.h"
 
 namespace cufk_amd {
@@ -177,21 +178,28 @@ __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const co
 // Every segment writes its total transform (row-major rotation, then translation; double) to
 // total[0..11].
 //
-// Loss: *loss also receives sum_i |x_i - target_i|^2 over the chain's points (target: the
-// chain's (points, 3) row), from the positions as stored (rounded to T), accumulated in double.
+// Loss (kLossSquared): *loss also receives sum_i |x_i - target_i|^2 over the chain's points
+// (target: the chain's (points, 3) row), from the positions as stored (rounded to T),
+// accumulated in double.  kLossSuperposed: record receives the sums and shift points of the
+// optimal superposition of the stored positions onto the target, which
+// superpose_records_kernel solves into the loss and the record the backward needs.
 //
 // Shadow (float16/bfloat16 whole chains): the positions are also stored unrounded, in float,
 // to shadow (the chain's (points, 3) row), and *regular receives the float32 chains' test
 // (FastPath<float>) on them, for the position-based backward over that copy.
-template <typename T, typename Lay, bool Segmented, bool Loss = false, bool Shadow = false>
+template <typename T, typename Lay, bool Segmented, int LossKind = kLossNone, bool Shadow = false>
 __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                               const T* __restrict__ Dr, const T* __restrict__ p0,
                                               const T* __restrict__ first_direction,
                                               const T* __restrict__ initial_normal, T* __restrict__ out,
                                               uint8_t* __restrict__ regular, int points, bool head,
                                               double* __restrict__ total, const T* __restrict__ target = nullptr,
-                                              T* __restrict__ loss = nullptr, float* __restrict__ shadow = nullptr) {
+                                              T* __restrict__ loss = nullptr, float* __restrict__ shadow = nullptr,
+                                              double* __restrict__ record = nullptr) {
   using R = compute_t<T>;
+  constexpr bool Loss = LossKind != kLossNone;
+  constexpr bool Superposed = LossKind == kLossSuperposed;
+  static_assert(!Loss || !Segmented, "the fused losses take whole chains");
   static_assert(!Shadow || (!Segmented && !Loss && std::is_same_v<R, float>), "shadow rows: whole half-type chains");
   using Fast = std::conditional_t<Shadow, FastPath<R>, FastPath<T>>;
   constexpr int W = Lay::kWaves;
@@ -290,7 +298,13 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
 
   R xmax = R(0);
-  double acc = 0.0;  // Loss: this thread's share of sum |x - target|^2
+  // The fused loss's share of this thread; superposed sums about the stored x2 and the
+  // target's point 2.
+  LossAccumulator<LossKind, R> lossacc;
+  if constexpr (Superposed) {
+    lossacc.cx = {widen(narrow<T>(p2.x)), widen(narrow<T>(p2.y)), widen(narrow<T>(p2.z))};
+    lossacc.ct = {widen(target[6]), widen(target[7]), widen(target[8])};
+  }
   {
     const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
@@ -299,8 +313,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
         if constexpr (Loss) {
           const V3<R> xs = {widen(narrow<T>(x.x)), widen(narrow<T>(x.y)), widen(narrow<T>(x.z))};
-          const V3<R> d = xs - V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]};
-          acc += static_cast<double>(dot(d, d));
+          lossacc.add(xs, V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]});
         }
         stage[o0 + 3 * i] = x.x;
         stage[o0 + 3 * i + 1] = x.y;
@@ -314,8 +327,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
           const V3<R> xs = {widen(narrow<T>(h[j].x)), widen(narrow<T>(h[j].y)), widen(narrow<T>(h[j].z))};
-          const V3<R> d = xs - V3<R>{widen(target[3 * j]), widen(target[3 * j + 1]), widen(target[3 * j + 2])};
-          acc += static_cast<double>(dot(d, d));
+          lossacc.add(xs, V3<R>{widen(target[3 * j]), widen(target[3 * j + 1]), widen(target[3 * j + 2])});
         }
       }
       stage[0] = ff.p0.x; stage[1] = ff.p0.y; stage[2] = ff.p0.z;
@@ -357,18 +369,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     }
     *regular = reg ? 1 : 0;
   }
-  if constexpr (Loss) {
-    __shared__ double loss_part[W];
-    acc = wave_sum(acc);
-    if (lane == 0) loss_part[wave] = acc;
-    __syncthreads();
-    if (tid == 0) {
-      double sum = 0.0;
-#pragma unroll
-      for (int w = 0; w < W; ++w) sum += loss_part[w];
-      *loss = narrow<T>(static_cast<R>(sum));
-    }
-  }
+  if constexpr (Loss) lossacc.template finish<T, W>(loss, record, lane, wave, tid);
   store_point_row<Lay>(out, stage, points, tid, !Segmented || head);
   if constexpr (Shadow) store_point_row<Lay>(shadow, stage, points, tid);
 }
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_forward_shadow_kernel(
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     T* __restrict__ xyz, float* __restrict__ shadow, uint8_t* __restrict__ regular, int points) {
   const int64_t row = blockIdx.x;
-  forward_chain<T, Layout<W, K, Pad>, false, false, true>(
+  forward_chain<T, Layout<W, K, Pad>, false, kLossNone, true>(
       lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0, first_direction,
       initial_normal, xyz + row * points * 3, regular + row, points, true, nullptr, nullptr, nullptr,
       shadow + row * points * 3);
@@ -601,17 +602,19 @@ __device__ __forceinline__ void exact_chain(const T* __restrict__ Lr, const T* _
 // gradients and the carry are turned to the local axes; only the head writes the
 // first-frame terms.
 //
-// Residual: gs holds a target row and the gradient is w2 (x - target), formed as the lane
-// loads its points (the coordinate loss's backward).
-template <typename T, typename Lay, bool Segmented = false, bool Residual = false>
+// Res (the fused losses' backward): gs holds a target row and the gradient of point x with
+// target t is res(x, t) (SquaredResidual, SuperposedResidual), formed as the lane loads its
+// points; NoResidual: gs holds the gradient row itself.
+template <typename T, typename Lay, bool Segmented = false, typename Res = NoResidual>
 __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restrict__ gAr, T* __restrict__ gDr,
                                                  compute_t<T>* xs, compute_t<T>* gs,
                                                  compute_t<T> (&wave_sum)[Lay::kWaves][6], int points,
                                                  double* __restrict__ anchor = nullptr, bool head = true,
                                                  const double* __restrict__ frame = nullptr,
                                                  const double* __restrict__ carry = nullptr,
-                                                 compute_t<T> bond1 = 0, compute_t<T> w2 = 0) {
+                                                 compute_t<T> bond1 = 0, const Res& res = Res{}) {
   using R = compute_t<T>;
+  constexpr bool Residual = !std::is_same_v<Res, NoResidual>;
   constexpr int W = Lay::kWaves;
   constexpr int K = Lay::kItems;
   const int steps = points - 3;
@@ -643,7 +646,13 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
     for (int i = 0; i < 3 * K; ++i) xr[9 + i] = xs[o0 + i];
     if constexpr (Residual) {
 #pragma unroll
-      for (int i = 0; i < 3 * K; ++i) gr[i] = w2 * (xr[9 + i] - gr[i]);
+      for (int i = 0; i < K; ++i) {
+        const V3<R> g = res(V3<R>{xr[9 + 3 * i], xr[10 + 3 * i], xr[11 + 3 * i]},
+                            V3<R>{gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]});
+        gr[3 * i] = g.x;
+        gr[3 * i + 1] = g.y;
+        gr[3 * i + 2] = g.z;
+      }
     }
   }
   double q[9];  // Segmented, after the head: the world rotation at x2
@@ -714,7 +723,7 @@ __device__ __forceinline__ void position_adjoint(T* __restrict__ gLr, T* __restr
     const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
     auto grad = [&](int j) {
       const V3<R> g = load3(&gs[3 * j]);
-      if constexpr (Residual) return w2 * (load3(&xs[3 * j]) - g);
+      if constexpr (Residual) return res(load3(&xs[3 * j]), g);
       return g;
     };
     const V3<R> g1 = grad(1);
@@ -1023,25 +1032,43 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_forward_kernel(
     const T* __restrict__ target, T* __restrict__ xyz, uint8_t* __restrict__ regular, T* __restrict__ loss,
     int points) {
   const int64_t row = blockIdx.x;
-  forward_chain<T, Layout<W, K, Pad>, false, true>(lengths + row * (points - 1), angles + row * (points - 2),
+  forward_chain<T, Layout<W, K, Pad>, false, kLossSquared>(lengths + row * (points - 1), angles + row * (points - 2),
                                                    dihedrals + row * (points - 3), p0, first_direction, initial_normal,
                                                    xyz + row * points * 3, regular + row, points, true, nullptr,
                                                    target + row * points * 3, loss + row);
 }
 
-// Its backward over the saved positions: the gradient row 2 w_b (x - target) is formed in LDS
-// from the staged positions and target (grad_xyz never exists in HBM), then the
-// position-based adjoint for regular chains and the exact one for the others, as in
-// reconstruct_backward_saved_kernel.
+// Forward of the superposed losses: the flagged forward, plus the sums of the optimal
+// superposition onto the target in each chain's record (superpose_records_kernel follows).
 template <typename T, int W, int K, int Pad>
+__global__ __launch_bounds__(64 * W) void reconstruct_superposed_forward_kernel(
+    const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
+    const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
+    const T* __restrict__ target, T* __restrict__ xyz, uint8_t* __restrict__ regular, double* __restrict__ record,
+    int points) {
+  const int64_t row = blockIdx.x;
+  forward_chain<T, Layout<W, K, Pad>, false, kLossSuperposed>(
+      lengths + row * (points - 1), angles + row * (points - 2), dihedrals + row * (points - 3), p0, first_direction,
+      initial_normal, xyz + row * points * 3, regular + row, points, true, nullptr, target + row * points * 3, nullptr,
+      nullptr, record + row * kSuperposeRecord);
+}
+
+// The backward of the fused losses over the saved positions: the gradient row is formed from
+// the staged positions and target (grad_xyz never exists in HBM), in registers as the
+// position-based adjoint loads them for regular chains, in LDS before the exact adjoint for the
+// others.  kLossSquared: 2 w_b (x - target).  kLossSuperposed: c (x - M t - a) from the
+// chain's superposition record (superpose.h), c = (2/N) w_b, divided by 2 rmsd unless
+// `squared` (0 where rmsd = 0).
+template <typename T, int W, int K, int Pad, int LossKind = kLossSquared>
 __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ target,
     const T* __restrict__ grad_loss, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points) {
+    T* __restrict__ grad_dihedrals, int points, const double* __restrict__ record = nullptr, int squared = 0) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
+  using Res = std::conditional_t<LossKind == kLossSuperposed, SuperposedResidual<R>, SquaredResidual<R>>;
   constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
   __shared__ __align__(16) R region_a[kA];
   __shared__ __align__(16) R region_b[Lay::kPointRow];
@@ -1055,18 +1082,23 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
     const T* const src[2] = {xyz + row * points * 3, target + row * points * 3};
     load_point_rows<Lay, 2>(dst, src, points, tid);
   }
+  const R w = grad_loss != nullptr ? widen(grad_loss[row]) : R(1);
+  const Res res = make_residual<LossKind>(w, record != nullptr ? record + row * kSuperposeRecord : nullptr, points,
+                                          squared);
   __syncthreads();
-  const R w2 = R(2) * (grad_loss != nullptr ? widen(grad_loss[row]) : R(1));
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
   T* gDr = grad_dihedrals + row * (points - 3);
   if (FastPath<T>::kEnabled && regular[row] != 0) {
-    position_adjoint<T, Lay, false, true>(gLr, gAr, gDr, region_a, region_b, wave_sum, points, nullptr, true, nullptr,
-                                          nullptr, R(0), w2);
+    position_adjoint<T, Lay, false, Res>(gLr, gAr, gDr, region_a, region_b, wave_sum, points, nullptr, true, nullptr,
+                                         nullptr, R(0), res);
   } else {
-    for (int e = tid; e < 3 * points; e += Lay::kLanes) {
-      const int slot = Lay::point_slot(e);
-      region_b[slot] = w2 * (region_a[slot] - region_b[slot]);
+    for (int p = tid; p < points; p += Lay::kLanes) {
+      const int slot = Lay::point_slot(3 * p);  // a point's three coordinates share a lane segment
+      const V3<R> g = res(load3(&region_a[slot]), load3(&region_b[slot]));
+      region_b[slot] = g.x;
+      region_b[slot + 1] = g.y;
+      region_b[slot + 2] = g.z;
     }
     __syncthreads();
     exact_chain<T, Lay, false, false>(lengths + row * (points - 1), angles + row * (points - 2),

@@ -14,6 +14,7 @@
 #include <type_traits>
 
 #include "chain_ops.h"
+#include "fused_loss.h"
 #include "staging.h"
 
 namespace cufk_amd {
@@ -83,10 +84,17 @@ __device__ __forceinline__ void load_pair_rows(compute_t<T>* __restrict__ srow, 
   }
 }
 
-// Forward (torsion.cu:254-295).
-template <typename T, int W, int K>
+// Forward (torsion.cu:254-295).  With LossKind (fused_loss.h) it also reduces the chain's loss
+// against target (its (points, 3) row) from the positions as stored: the sum of squares into
+// loss[row], or the superposition sums into the chain's record (superpose_records_kernel
+// follows).
+template <typename T, int W, int K, int LossKind = kLossNone>
 __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __restrict__ raw_pairs, int64_t raw_stride,
-                                                                 TorsionArgs cst, T* __restrict__ xyz, int points) {
+                                                                 TorsionArgs cst, T* __restrict__ xyz, int points,
+                                                                 const T* __restrict__ target = nullptr,
+                                                                 T* __restrict__ loss = nullptr,
+                                                                 double* __restrict__ record = nullptr) {
+  constexpr bool Loss = LossKind != kLossNone;
   static_assert(K % 12 == 0, "torsion plans keep phases lane-invariant and segments 16-byte aligned");
   using R = compute_t<T>;
   using Lay = Layout<W, K, 1>;
@@ -103,13 +111,20 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
   const int wave = tid >> 6;
 
   load_pair_rows<Lay>(stage, stage + Lay::kStepRow, raw, steps, tid);
+  const int s0 = tid * K;
+  const T* tgt = Loss ? target + row * points * 3 : nullptr;
+  // The target of the lane's own points, loaded now so that the scan hides the latency.
+  R tr[Loss ? 3 * K : 1];
+  if constexpr (Loss) {
+    const int count = steps - s0 < K ? (steps - s0 > 0 ? steps - s0 : 0) : K;
+    load_run<3 * K>(tgt + 9 + 3 * s0, 3 * count, tr);
+  }
   __syncthreads();
 
   // Serial part in double with the float64 bond-angle sin/cos (the reference rounds them to
   // the compute type, torsion.cu:226-227, which biases |M| per phase along the chain).
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
-  const int s0 = tid * K;
   const int b0 = Lay::lane_step_base(tid);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
@@ -142,11 +157,18 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
   const V3<R> gv = {p2.x + (-c0a * excl.v[0] - s0a * excl.v[1]), p2.y + (s0a * excl.v[0] - c0a * excl.v[1]),
                     p2.z + excl.v[2]};
 
+  LossAccumulator<LossKind, R> lossacc;
+  auto stored = [](V3<R> x) { return V3<R>{widen(narrow<T>(x.x)), widen(narrow<T>(x.y)), widen(narrow<T>(x.z))}; };
+  if constexpr (LossKind == kLossSuperposed) {
+    lossacc.cx = stored(p2);
+    lossacc.ct = {widen(tgt[6]), widen(tgt[7]), widen(tgt[8])};
+  }
   const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (s0 + i < steps) {
       const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+      if constexpr (Loss) lossacc.add(stored(x), V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]});
       stage[o0 + 3 * i] = x.x;
       stage[o0 + 3 * i + 1] = x.y;
       stage[o0 + 3 * i + 2] = x.z;
@@ -156,8 +178,19 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
     stage[0] = R(0); stage[1] = R(0); stage[2] = R(0);
     stage[3] = l0;   stage[4] = R(0); stage[5] = R(0);
     stage[6] = p2.x; stage[7] = p2.y; stage[8] = p2.z;
+    if constexpr (Loss) {
+      const V3<R> h[3] = {{R(0), R(0), R(0)}, {l0, R(0), R(0)}, p2};
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        lossacc.add(stored(h[j]), V3<R>{widen(tgt[3 * j]), widen(tgt[3 * j + 1]), widen(tgt[3 * j + 2])});
+    }
   }
-  __syncthreads();
+  if constexpr (Loss) {
+    lossacc.template finish<T, W>(loss != nullptr ? loss + row : nullptr,
+                                  record != nullptr ? record + row * kSuperposeRecord : nullptr, lane, wave, tid);
+  } else {
+    __syncthreads();
+  }
   store_point_row<Lay>(out, stage, points, tid);
 }
 
@@ -170,11 +203,18 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
 // of the suffix scan go through LDS.  With K = 3 (the smallest multiple of the phase period)
 // a workgroup per chain holds up to eight waves per SIMD, where staging whole rows through
 // LDS held one or two.
-template <typename T, int W, int K>
+//
+// With LossKind (fused_loss.h) grad_xyz is the loss's target row instead, and the gradient of
+// each point is formed from its position and target as the lane loads them (grad_loss: the
+// upstream weight per chain, or NULL for ones; record: the superposed kinds' records).
+template <typename T, int W, int K, int LossKind = kLossNone>
 __global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __restrict__ raw_pairs, int64_t raw_stride,
                                                                   const T* __restrict__ xyz, const T* __restrict__ grad_xyz,
                                                                   T* __restrict__ grad_raw, int64_t grad_raw_stride,
-                                                                  TorsionArgs cst, int points) {
+                                                                  TorsionArgs cst, int points,
+                                                                  const T* __restrict__ grad_loss = nullptr,
+                                                                  const double* __restrict__ record = nullptr,
+                                                                  int squared = 0) {
   static_assert(K % 3 == 0, "torsion plans keep phases lane-invariant");
   using R = compute_t<T>;
   __shared__ R wave_sum[W][6];
@@ -196,6 +236,19 @@ __global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __res
   load_run<3 * K + 9>(Xr + 3 * s0, count > 0 ? 3 * (count + 3) : 0, xr);
   load_run<3 * K>(Gr + 9 + 3 * s0, 3 * count, gr);
   load_run<2 * K>(raw + 2 * s0, 2 * count, pr);
+  if constexpr (LossKind != kLossNone) {  // gr holds the target: form each point's gradient
+    const R w = grad_loss != nullptr ? widen(grad_loss[row]) : R(1);
+    const auto res = make_residual<LossKind>(w, record != nullptr ? record + row * kSuperposeRecord : nullptr, points,
+                                             squared);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const V3<R> g = res(V3<R>{xr[9 + 3 * i], xr[10 + 3 * i], xr[11 + 3 * i]},
+                          V3<R>{gr[3 * i], gr[3 * i + 1], gr[3 * i + 2]});
+      gr[3 * i] = g.x;
+      gr[3 * i + 1] = g.y;
+      gr[3 * i + 2] = g.z;
+    }
+  }
   const V3<R> c = {widen(Xr[6]), widen(Xr[7]), widen(Xr[8])};
   auto pos = [&](int j) { return V3<R>{xr[3 * j], xr[3 * j + 1], xr[3 * j + 2]} - c; };
 

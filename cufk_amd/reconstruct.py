@@ -132,8 +132,9 @@ def reconstruct_loss(
     fused with it.
 
     Equal to ``((reconstruct(lengths, angles, dihedrals, ...) - target) ** 2).sum((-2, -1))``,
-    but the coordinates never reach memory: the forward returns only the loss, and the
-    backward recomputes the positions and forms their gradient inside the kernel.
+    but ``grad_xyz`` never exists in memory: the forward reduces the loss from the positions in
+    registers (it also writes the positions, kept for the backward, not returned), and the
+    backward forms each point's gradient from its saved position and target inside the kernel.
 
     Args:
         lengths, angles, dihedrals, p0, first_direction, initial_normal: as for
@@ -158,5 +159,55 @@ def reconstruct_loss(
         p0,
         first_direction,
         initial_normal,
+    )
+    return loss[0] if single else loss
+
+
+def reconstruct_rmsd(
+    lengths: torch.Tensor,
+    angles: torch.Tensor,
+    dihedrals: torch.Tensor,
+    target: torch.Tensor,
+    p0: torch.Tensor | None = None,
+    first_direction: torch.Tensor | None = None,
+    initial_normal: torch.Tensor | None = None,
+    *,
+    squared: bool = False,
+) -> torch.Tensor:
+    r"""Per-chain RMSD of the reconstruction from ``target`` after optimal superposition, fused
+    with the reconstruction.
+
+    For each chain, :math:`\min_R \sqrt{\tfrac1N \sum_i \lVert R (x_i - \bar x) - (t_i - \bar t)
+    \rVert^2}` over proper rotations (the Kabsch / Horn superposition, solved per chain in double
+    inside the forward kernel), or the mean squared deviation itself with ``squared=True``.  The
+    backward forms ``grad_xyz`` inside the kernel from the saved positions, the target and the
+    chain's optimal rotation (the rotation's own dependence drops out at the optimum), so it
+    never exists in memory.  Where the RMSD is 0 its gradient is taken as 0.
+
+    Args:
+        lengths, angles, dihedrals, p0, first_direction, initial_normal: as for
+            :func:`reconstruct` (4 <= N <= 2051).
+        target: ``(N, 3)`` or ``(B, N, 3)``, dtype and device of ``lengths``; no gradient.
+        squared: return the mean squared deviation instead of its square root.
+
+    Returns:
+        ``(B,)`` values, or a 0-d tensor for one chain; the positions as stored (rounded to the
+        dtype) are the ones superposed.  The reference has no counterpart.
+    """
+    lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
+    if single:
+        target = target[None]
+    p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
+    first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
+    initial_normal = _anchor(initial_normal, (0.0, 0.0, 1.0), lengths)
+    loss = _C.apply_superposed(
+        lengths.contiguous(),
+        angles.contiguous(),
+        dihedrals.contiguous(),
+        target.contiguous(),
+        p0,
+        first_direction,
+        initial_normal,
+        1 if squared else 2,
     )
     return loss[0] if single else loss

@@ -26,6 +26,35 @@ class TorsionReconstructor(Protocol):
         ...
 
 
+class _TorsionCall:
+    """The callable ``compile_torsion`` returns: calling it is the reference's module ``apply``
+    (torsion.py:134-135).  ``loss`` and ``rmsd`` are extensions with no reference counterpart:
+    the torsion path fused with a per-chain loss against a target, whose backward forms
+    ``grad_xyz`` inside the kernel (the reference's torsion backward, torsion.cu:297-381, reads
+    a materialised one)."""
+
+    __slots__ = ("_module", "_apply")
+
+    def __init__(self, module):
+        self._module = module
+        self._apply = module.apply
+
+    def __call__(self, raw_pairs: torch.Tensor) -> torch.Tensor:
+        return self._apply(raw_pairs)
+
+    def loss(self, raw_pairs: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        r"""Per-chain :math:`\sum_i \lVert x_i - t_i \rVert^2` of the reconstruction of
+        ``raw_pairs`` against ``target`` ``(B, N, 3)`` (same dtype and device, no gradient),
+        ``(B,)``; gradients flow to ``raw_pairs``."""
+        return self._module.loss(raw_pairs, target.contiguous(), 0)
+
+    def rmsd(self, raw_pairs: torch.Tensor, target: torch.Tensor, squared: bool = False) -> torch.Tensor:
+        r"""Per-chain RMSD of the reconstruction from ``target`` after optimal superposition (the
+        mean squared deviation with ``squared=True``), ``(B,)``; as
+        :func:`cufk_amd.reconstruct_rmsd` for the torsion path."""
+        return self._module.loss(raw_pairs, target.contiguous(), 1 if squared else 2)
+
+
 _TORSION_CALLS: dict[tuple[tuple[float, float, float], tuple[float, float, float]], TorsionReconstructor] = {}
 _TORSION_MODULES: dict[tuple[tuple[float, float, float], tuple[float, float, float]], object] = {}
 
@@ -65,7 +94,8 @@ def compile_torsion(
 
     Returns:
         A cached callable ``reconstruct(raw_pairs) -> xyz``.  Equal arguments return the
-        same callable object.
+        same callable object.  It also offers the fused losses ``.loss(raw_pairs, target)``
+        and ``.rmsd(raw_pairs, target, squared=False)`` (extensions).
     """
     lengths = _as_triple(bond_lengths, "bond_lengths")
     angles = _as_triple(bond_angles, "bond_angles")
@@ -73,5 +103,5 @@ def compile_torsion(
     if key not in _TORSION_CALLS:
         module = _C.TorsionModule(*_constants(lengths, angles))
         _TORSION_MODULES[key] = module
-        _TORSION_CALLS[key] = module.apply
+        _TORSION_CALLS[key] = _TorsionCall(module)
     return _TORSION_CALLS[key]

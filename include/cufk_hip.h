@@ -42,8 +42,20 @@ enum cufk_status {
   CUFK_ERR_LAUNCH = 7,      /* kernel launch failed (C10_CUDA_KERNEL_LAUNCH_CHECK, block.cu:327) */
   CUFK_ERR_DEVICE = 8,      /* device query failed */
   CUFK_ERR_SEGMENT = 9,     /* long-chain segment length outside [1, 2048] */
-  CUFK_ERR_SCRATCH = 10     /* batch larger than the static scratch of an allocation-free entry point */
+  CUFK_ERR_SCRATCH = 10,    /* batch larger than the static scratch of an allocation-free entry point */
+  CUFK_ERR_LOSS = 11        /* unknown or unsupported loss kind */
 };
+
+/* Fused loss kinds (cufk_torsion_loss_*, cufk_reconstruct_superposed_*). */
+enum cufk_loss {
+  CUFK_LOSS_SQUARED_DISTANCE = 0, /* sum_i |x_i - t_i|^2 */
+  CUFK_LOSS_MSD = 1,              /* mean squared deviation after optimal superposition */
+  CUFK_LOSS_RMSD = 2              /* its square root: the RMSD */
+};
+/* Doubles per chain of a superposition record: the optimal rotation's transpose (row-major),
+ * xbar - R^T tbar, and the mean squared deviation (the rest is working space); written by the
+ * forward, read by the backward. */
+#define CUFK_SUPERPOSITION_DOUBLES 24
 
 /* Chains per call of cufk_reconstruct_bwd_anchored_noalloc (its static scratch: 6 doubles each). */
 #define CUFK_NOALLOC_MAX_CHAINS 65536
@@ -212,6 +224,45 @@ int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles
                               const uint8_t* chain_regular, const void* target, const void* grad_loss,
                               void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
                               int64_t points, void* stream);
+
+/*
+ * Fused superposed losses: loss[b] = min over rotations R of (1/N) sum_i |R (x_i - xbar) -
+ * (t_i - tbar)|^2 (CUFK_LOSS_MSD), or its square root (CUFK_LOSS_RMSD), x the reconstruction of
+ * (lengths, angles, dihedrals, anchors) as stored (rounded to the dtype) and t = target (B, N, 3).
+ * The optimal rotation comes from Horn's quaternion method, solved per chain in double inside the
+ * forward; no reference counterpart (the reference leaves losses to PyTorch).  The forward
+ * writes xyz and chain_regular as cufk_reconstruct_fwd_flagged does, loss (B,) and
+ * superposition (B x CUFK_SUPERPOSITION_DOUBLES doubles).  The backward takes them (same
+ * loss_kind) with grad_loss (B,) or NULL (ones) and forms grad_xyz = c (x_i - R^T (t_i - tbar) -
+ * xbar) per point inside the kernel, c = (2/N) grad_loss[b] (divided by 2 rmsd for the RMSD; 0
+ * where rmsd = 0).  4 <= N <= 2051.
+ */
+int cufk_reconstruct_superposed_fwd(int dtype, int loss_kind, const void* lengths, const void* angles,
+                                    const void* dihedrals, const void* p0, const void* first_direction,
+                                    const void* initial_normal, const void* target, void* xyz, uint8_t* chain_regular,
+                                    void* loss, double* superposition, int64_t batch, int64_t points, void* stream);
+int cufk_reconstruct_superposed_bwd(int dtype, int loss_kind, const void* lengths, const void* angles,
+                                    const void* dihedrals, const void* p0, const void* first_direction,
+                                    const void* initial_normal, const void* xyz, const uint8_t* chain_regular,
+                                    const void* target, const double* superposition, const void* grad_loss,
+                                    void* grad_lengths, void* grad_angles, void* grad_dihedrals, int64_t batch,
+                                    int64_t points, void* stream);
+
+/*
+ * Torsion path with a fused loss of any cufk_loss kind against target (B, N, 3).  The forward
+ * is cufk_torsion_fwd plus loss (B,) and, for the superposed kinds, superposition (B x
+ * CUFK_SUPERPOSITION_DOUBLES; NULL allowed for CUFK_LOSS_SQUARED_DISTANCE).  The backward is
+ * cufk_torsion_bwd with grad_xyz formed inside the kernel from the saved xyz and the target
+ * (torsion.cu:297-381 consumes a materialised grad_xyz), grad_loss (B,) or NULL (ones).  No
+ * reference counterpart.
+ */
+int cufk_torsion_loss_fwd(int dtype, int loss_kind, const void* raw_pairs, int64_t raw_stride,
+                          const cufk_torsion_consts* consts, const void* target, void* xyz, void* loss,
+                          double* superposition, int64_t batch, int64_t points, void* stream);
+int cufk_torsion_loss_bwd(int dtype, int loss_kind, const void* raw_pairs, int64_t raw_stride, const void* xyz,
+                          const void* target, const double* superposition, const void* grad_loss, void* grad_raw,
+                          int64_t grad_raw_stride, const cufk_torsion_consts* consts, int64_t batch, int64_t points,
+                          void* stream);
 
 /*
  * Long chains (any N >= 4; no step cap).  The reference stops at 2048 local transforms

@@ -28,6 +28,11 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
   branch, and torch.autograd through the torch restatement with its anchors.
 * ``torsion_constants``: closed form (float rounding of lengths, float64
   ``math.sin``/``math.cos`` of the angles printed with ``.17g``).
+* ``superpose`` / ``superposed_loss`` / ``superposed_grad_xyz`` (the fused RMSD losses, no
+  reference counterpart): zero for rigidly moved copies, invariance under rigid motions of
+  either side and symmetry in its arguments, a proper rotation for mirrored targets, a brute
+  search over rotations, central finite differences of the loss in x and, composed with the
+  forward and backward, in the internal coordinates.
 
 No reference golden vectors exist (the reference ships no tests), so parity of
 bit-level fp32/fp16/bf16 rounding with the CUDA build is unpinned; those
@@ -507,6 +512,56 @@ def torsion_backward(raw_pairs, xyz, grad_xyz, consts: TorsionConstants):
     out[:, 0::2] = rc * scale
     out[:, 1::2] = -rs * scale
     return out
+
+
+# ---------------------------------------------------------------- superposed losses
+#
+# No reference counterpart (the reference leaves losses to PyTorch): the fused RMSD losses of
+# cufk_amd.  Restated here with the SVD form of the Kabsch algorithm (W. Kabsch, Acta Cryst. A32,
+# 1976; A34, 1978), an independent route from the kernels' quaternion eigenproblem.
+
+
+def superpose(xyz, target):
+    """Optimal proper rotation of each chain onto its target: returns R (B, 3, 3) with
+    R (x_i - xbar) ~ t_i - tbar, the centroids xbar, tbar (B, 3) and the mean squared deviation
+    after superposition (B,)."""
+    x = np.asarray(xyz, np.float64)
+    t = np.asarray(target, np.float64)
+    xb, tb = x.mean(axis=1), t.mean(axis=1)
+    xc, tc = x - xb[:, None], t - tb[:, None]
+    H = np.einsum("bia,bic->bac", xc, tc)  # sum_i x'_a t'_c
+    U, _, Vt = np.linalg.svd(H)
+    d = np.sign(np.linalg.det(np.einsum("bji,bkj->bik", Vt, U)))  # det(V U^T)
+    d = np.where(d == 0, 1.0, d)
+    D = np.zeros_like(H)
+    D[:, 0, 0] = D[:, 1, 1] = 1.0
+    D[:, 2, 2] = d
+    R = np.einsum("bji,bjk,blk->bil", Vt, D, U)  # V D U^T
+    resid = np.einsum("bac,bic->bia", R, xc) - tc
+    msd = np.mean(np.sum(resid**2, axis=-1), axis=1)
+    return R, xb, tb, msd
+
+
+def superposed_loss(xyz, target, squared=False):
+    """Per-chain mean squared deviation after optimal superposition, or its square root."""
+    msd = superpose(xyz, target)[3]
+    return msd if squared else np.sqrt(msd)
+
+
+def superposed_grad_xyz(xyz, target, grad_loss=None, squared=False):
+    """dL/dx of the superposed loss: (2/N) w ((x_i - xbar) - R^T (t_i - tbar)), divided by
+    2 rmsd for the RMSD (0 where it is 0).  The rotation's own dependence on x drops out at
+    the optimum (envelope theorem)."""
+    x = np.asarray(xyz, np.float64)
+    R, xb, tb, msd = superpose(x, target)
+    n = x.shape[1]
+    w = np.ones(x.shape[0]) if grad_loss is None else np.asarray(grad_loss, np.float64)
+    c = 2.0 * w / n
+    if not squared:
+        rmsd = np.sqrt(msd)
+        c = np.where(rmsd > 0, c / (2.0 * np.where(rmsd > 0, rmsd, 1.0)), 0.0)
+    tc = np.asarray(target, np.float64) - tb[:, None]
+    return c[:, None, None] * ((x - xb[:, None]) - np.einsum("bca,bic->bia", R, tc))
 
 
 # ---------------------------------------------------------------- synthetic inputs

@@ -29,6 +29,10 @@ def lib():
     lib.cufk_torsion_bwd.argtypes = [ctypes.c_int, vp, i64, vp, vp, vp, i64, vp, i64, i64, vp]
     lib.cufk_reconstruct_bwd_anchored.argtypes = [ctypes.c_int] + [vp] * 16 + [i64, i64, vp]
     lib.cufk_reconstruct_bwd_anchored_noalloc.argtypes = [ctypes.c_int] + [vp] * 15 + [i64, i64, vp]
+    lib.cufk_reconstruct_superposed_fwd.argtypes = [ctypes.c_int, ctypes.c_int] + [vp] * 11 + [i64, i64, vp]
+    lib.cufk_reconstruct_superposed_bwd.argtypes = [ctypes.c_int, ctypes.c_int] + [vp] * 14 + [i64, i64, vp]
+    lib.cufk_torsion_loss_fwd.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, vp, vp, vp, vp, vp, i64, i64, vp]
+    lib.cufk_torsion_loss_bwd.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, vp, vp, vp, vp, vp, i64, vp, i64, i64, vp]
     lib.cufk_reconstruct_loss_fwd.argtypes = [ctypes.c_int] + [vp] * 10 + [i64, i64, vp]
     lib.cufk_reconstruct_loss_bwd.argtypes = [ctypes.c_int] + [vp] * 13 + [i64, i64, vp]
     lib.cufk_reconstruct_long_fwd.argtypes = [ctypes.c_int] + [vp] * 8 + [i64, i64, i64, vp]
@@ -72,8 +76,12 @@ def test_header_declares_the_entry_points():
         "cufk_reconstruct_loss_bwd",
         "cufk_reconstruct_loss_fwd",
         "cufk_reconstruct_shadow_floats",
+        "cufk_reconstruct_superposed_bwd",
+        "cufk_reconstruct_superposed_fwd",
         "cufk_torsion_bwd",
         "cufk_torsion_fwd",
+        "cufk_torsion_loss_bwd",
+        "cufk_torsion_loss_fwd",
         "cufk_version",
     ]
 
@@ -246,3 +254,34 @@ def test_anchored_noalloc_status_paths(lib):
     assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 65537, 10, null) == ERR_SCRATCH
     assert f(0, p, p, p, p, p, p, p, p, p, p, p, p, p, p, p, 65537, 3, null) == ERR_POINTS
     assert lib.cufk_error_string(ERR_SCRATCH).startswith(b"batch exceeds the 65536 chains")
+
+
+ERR_LOSS = 11
+
+
+def test_fused_loss_status_paths(lib):
+    """Loss kinds, shapes and pointers are checked before any device work."""
+    p = ctypes.c_void_p(1)
+    null = None
+    f = lib.cufk_reconstruct_superposed_fwd
+    #        dtype kind L  A  D  p0 d0 n0 tgt xyz flags loss rec
+    assert f(0, 0, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_LOSS  # squared distance: reconstruct_loss
+    assert f(0, 3, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_LOSS
+    assert f(9, 2, p, p, p, p, p, p, p, p, p, p, p, 4, 10, null) == ERR_DTYPE
+    assert f(0, 2, p, p, p, p, p, p, p, p, p, p, null, 4, 10, null) == ERR_NULL  # the record is required
+    assert f(0, 1, p, p, p, p, p, p, p, p, p, p, p, 4, 3, null) == ERR_POINTS
+    assert f(0, 1, p, p, p, p, p, p, p, p, p, p, null, 0, 10, null) == OK  # empty batch: nothing to do
+    b = lib.cufk_reconstruct_superposed_bwd
+    #        dtype kind L  A  D  p0 d0 n0 xyz flags tgt rec gl gL gA gD
+    assert b(0, 2, p, p, p, p, p, p, p, p, p, null, null, p, p, p, 4, 10, null) == ERR_NULL
+    assert b(0, 2, p, p, p, p, p, p, p, p, p, p, null, p, p, p, 4, 2052, null) == ERR_STEPS
+    t = lib.cufk_torsion_loss_fwd
+    #        dtype kind raw stride consts tgt xyz loss rec
+    assert t(0, 4, p, 10, p, p, p, p, p, 4, 8, null) == ERR_LOSS
+    assert t(0, 0, p, -1, p, p, p, p, null, 4, 8, null) == ERR_STRIDE
+    assert t(0, 2, p, 10, p, p, p, p, null, 4, 8, null) == ERR_NULL  # superposed kinds need the record
+    tb = lib.cufk_torsion_loss_bwd
+    #         dtype kind raw stride xyz tgt rec gl graw gstride consts
+    assert tb(0, 1, p, 10, p, p, null, null, p, 10, p, 4, 8, null) == ERR_NULL
+    assert tb(0, 0, p, 10, p, p, null, null, p, -2, p, 4, 8, null) == ERR_STRIDE
+    assert lib.cufk_error_string(ERR_LOSS) == b"unknown or unsupported loss kind"

@@ -10,6 +10,7 @@ mistakes in copies of the oracle and show that these checks catch them.
 from __future__ import annotations
 
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -426,3 +427,212 @@ def test_cpu_torch_torsion_matches_the_oracle():
     gr = o.torsion_backward(raw, xr, g, c)
     got = ct.torsion_backward(torch.tensor(raw), x, torch.tensor(g), c.lengths)
     assert np.abs(got.numpy() - gr).max() <= 1e-10 * np.abs(gr).max()
+
+
+# ------------------------------------------------------------------ superposed losses
+
+
+def _rot(rng):
+    q, _ = np.linalg.qr(rng.normal(size=(3, 3)))
+    return q * np.sign(np.linalg.det(q))
+
+
+def test_superpose_zero_for_rigid_copies_and_invariant():
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(4, 30, 3)) * 2.0
+    Q = np.stack([_rot(rng) for _ in range(4)])
+    moved = np.einsum("bij,bkj->bki", Q, x) + rng.normal(size=(4, 1, 3)) * 5
+    assert np.abs(o.superposed_loss(x, moved, squared=True)).max() < 1e-20
+    t = rng.normal(size=x.shape)
+    base = o.superposed_loss(x, t)
+    Q2 = np.stack([_rot(rng) for _ in range(4)])
+    t_moved = np.einsum("bij,bkj->bki", Q2, t) - 3.0
+    assert np.allclose(o.superposed_loss(x, t_moved), base, rtol=1e-12)
+    assert np.allclose(o.superposed_loss(t, x), base, rtol=1e-12)  # symmetric in its arguments
+
+
+def test_superpose_is_a_proper_rotation_for_mirrored_targets():
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(3, 25, 3)) * [3.0, 2.0, 1.0]
+    mirrored = x * [1.0, 1.0, -1.0]  # a reflection: no proper rotation maps x onto it
+    R, _, _, msd = o.superpose(x, mirrored)
+    assert np.allclose(np.linalg.det(R), 1.0)
+    assert np.all(msd > 0.1)
+
+
+def test_superpose_beats_every_sampled_rotation():
+    """Optimality: no sampled proper rotation (uniform quaternions) and no small perturbation
+    of the solution does better."""
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(1, 40, 3))
+    t = np.einsum("ij,bkj->bki", _rot(rng), x) + 0.3 * rng.normal(size=x.shape)
+    R, xb, tb, msd = o.superpose(x, t)
+    xc, tc = x[0] - xb[0], t[0] - tb[0]
+
+    def msd_of(Rm):
+        return np.mean(np.sum((xc @ Rm.T - tc) ** 2, axis=1))
+
+    q = rng.normal(size=(20000, 4))
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    w, a, b, c = q.T
+    Rs = np.stack([np.stack([w*w+a*a-b*b-c*c, 2*(a*b-w*c), 2*(a*c+w*b)], -1),
+                   np.stack([2*(b*a+w*c), w*w-a*a+b*b-c*c, 2*(b*c-w*a)], -1),
+                   np.stack([2*(c*a-w*b), 2*(c*b+w*a), w*w-a*a-b*b+c*c], -1)], -2)
+    sampled = np.mean(np.sum((np.einsum("rij,kj->rki", Rs, xc) - tc) ** 2, axis=-1), axis=1)
+    assert msd[0] <= sampled.min() + 1e-12
+    for _ in range(20):
+        k = rng.normal(size=3) * 1e-3
+        K = np.array([[0, -k[2], k[1]], [k[2], 0, -k[0]], [-k[1], k[0], 0]])
+        assert msd_of(R[0] @ (np.eye(3) + K + K @ K / 2)) >= msd[0] - 1e-15
+
+
+@pytest.mark.parametrize("squared", [True, False])
+def test_superposed_gradient_finite_differences(squared):
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(2, 15, 3))
+    t = rng.normal(size=(2, 15, 3))
+    w = np.array([1.5, -0.5])
+    g = o.superposed_grad_xyz(x, t, w, squared)
+    h = 1e-6
+    for b, i, a in [(0, 0, 0), (0, 7, 2), (1, 14, 1), (1, 3, 0)]:
+        xp, xm = x.copy(), x.copy()
+        xp[b, i, a] += h
+        xm[b, i, a] -= h
+        fd = w[b] * (o.superposed_loss(xp, t, squared)[b] - o.superposed_loss(xm, t, squared)[b]) / (2 * h)
+        assert abs(fd - g[b, i, a]) <= 1e-7 * max(1.0, abs(fd))
+
+
+@pytest.mark.parametrize("squared", [True, False])
+def test_superposed_loss_through_the_chain_finite_differences(squared):
+    """The composition the fused kernels compute: the forward, the superposed loss, and the
+    reference backward fed with superposed_grad_xyz, against central differences in L, A, D."""
+    d = o.synthetic_inputs(2, 14, seed=9, anchors=True)
+    an = _anchors(d)
+    t = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+    t = t + np.random.default_rng(1).normal(0.0, 0.2, t.shape)
+
+    def loss(L, A, D):
+        return o.superposed_loss(o.reconstruct_forward(L, A, D, **an), t, squared).sum()
+
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+    grads = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], o.superposed_grad_xyz(x, t, None, squared),
+                                   **an)
+    h = 1e-6
+    for k, (name, g) in enumerate(zip(("lengths", "angles", "dihedrals"), grads)):
+        for b, j in [(0, 0), (1, 5), (0, g.shape[1] - 1)]:
+            args = [d["lengths"].copy(), d["angles"].copy(), d["dihedrals"].copy()]
+            args[k][b, j] += h
+            fp = loss(*args)
+            args[k][b, j] -= 2 * h
+            fm = loss(*args)
+            assert abs((fp - fm) / (2 * h) - g[b, j]) <= 1e-6 * max(1.0, abs(g[b, j])), (name, b, j)
+
+
+def test_torsion_losses_through_the_chain_finite_differences():
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    rng = np.random.default_rng(10)
+    raw = rng.normal(size=(2, 2 * 12))
+    t = o.torsion_forward(raw, c) + rng.normal(0.0, 0.2, (2, 15, 3))
+    x = o.torsion_forward(raw, c)
+    for kind in ("squared_distance", "msd", "rmsd"):
+        if kind == "squared_distance":
+            f = lambda r: ((o.torsion_forward(r, c) - t) ** 2).sum()  # noqa: E731
+            gx = 2.0 * (x - t)
+        else:
+            sq = kind == "msd"
+            f = lambda r: o.superposed_loss(o.torsion_forward(r, c), t, sq).sum()  # noqa: E731
+            gx = o.superposed_grad_xyz(x, t, None, sq)
+        g = o.torsion_backward(raw, x, gx, c)
+        h = 1e-6
+        for b, j in [(0, 0), (1, 7), (0, 23)]:
+            rp, rm = raw.copy(), raw.copy()
+            rp[b, j] += h
+            rm[b, j] -= h
+            fd = (f(rp) - f(rm)) / (2 * h)
+            # torsion_backward forms 1/l in float (torsion.cu:216), a 1e-8 relative effect.
+            assert abs(fd - g[b, j]) <= 1e-6 * max(1.0, abs(fd)), (kind, b, j)
+
+
+def test_superpose_header_matches_the_oracle(tmp_path):
+    """cufk_amd/csrc/superpose.h (Horn's quaternion eigenproblem, as the kernels run it) built
+    for the host with g++, against the SVD oracle: msd to 1e-10 relative, R^T and the offset
+    to 1e-9, for generic, well-fitted, mirrored and collinear chains."""
+    import shutil
+    import subprocess
+
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no host C++ compiler")
+    root = Path(__file__).resolve().parent.parent
+    src = tmp_path / "sp.cpp"
+    src.write_text(
+        '#include "superpose.h"\n#include <cstdio>\nusing namespace cufk_amd;\n'
+        "int main() { int n; double cx[3], ct[3];\n"
+        '  while (scanf("%d %lf %lf %lf %lf %lf %lf", &n, cx, cx + 1, cx + 2, ct, ct + 1, ct + 2) == 7) {\n'
+        "    double s[kSuperposeSums] = {};\n"
+        "    for (int i = 0; i < n; ++i) { double x[3], t[3];\n"
+        '      if (scanf("%lf %lf %lf %lf %lf %lf", x, x + 1, x + 2, t, t + 1, t + 2) != 6) return 1;\n'
+        "      for (int k = 0; k < 3; ++k) { x[k] -= cx[k]; t[k] -= ct[k]; }\n"
+        "      superpose_add(s, x, t); }\n"
+        "    double out[kSuperposeRecord]; superpose_solve(s, n, cx, ct, out);\n"
+        '    for (int i = 0; i < 13; ++i) printf("%.17g ", out[i]); printf("\\n"); }\n  return 0; }\n'
+    )
+    exe = tmp_path / "sp"
+    subprocess.run([gxx, "-O2", "-std=c++17", f"-I{root / 'cufk_amd' / 'csrc'}", str(src), "-o", str(exe)], check=True)
+    rng = np.random.default_rng(11)
+    cases = []
+    for n in (4, 5, 64, 400):
+        x = rng.normal(size=(n, 3)) * [3.0, 2.0, 1.0] + 4.0
+        cases.append((x, x @ _rot(rng).T + 0.2 * rng.normal(size=x.shape) - 6.0, True))
+    x = rng.normal(size=(50, 3))
+    cases.append((x, x @ _rot(rng).T + 1e-5 * rng.normal(size=x.shape), True))  # well fitted
+    cases.append((x, x * [1.0, -1.0, 1.0], True))  # mirrored
+    line = np.outer(np.arange(6.0), [1.0, 2.0, 0.5])
+    cases.append((line, rng.normal(size=(6, 3)), False))  # collinear chain: R is not unique
+    cases.append((x, x.copy(), True))  # identical: the identity, msd 0
+    cases.append((x, np.full_like(x, 1.5), False))  # target at one point: the key matrix is 0
+    square = np.array([[1.0, 1, 0], [-1, 1, 0], [-1, -1, 0], [1, -1, 0], [0.5, 0.2, 0]])
+    cases.append((square, -square, True))  # inversion of a planar set: a half turn about its normal
+    for k in range(200):  # fits from near-exact to pure noise
+        n = int(rng.integers(4, 80))
+        x = rng.normal(size=(n, 3)) * rng.uniform(0.5, 5.0, 3)
+        noise = 10.0 ** rng.uniform(-7, 1)
+        cases.append((x, x @ _rot(rng).T + noise * rng.normal(size=x.shape) + rng.normal(size=3) * 10, True))
+    text = ""
+    for x, t, _ in cases:
+        text += f"{len(x)} " + " ".join(repr(float(v)) for v in (*x[2], *t[2])) + "\n"
+        text += "\n".join(" ".join(repr(float(v)) for v in (*a, *b)) for a, b in zip(x, t)) + "\n"
+    out = subprocess.run([str(exe)], input=text, capture_output=True, text=True, check=True).stdout.split("\n")
+    for (x, t, unique), line_out in zip(cases, out):
+        got = np.array([float(v) for v in line_out.split()])
+        R, xb, tb, msd = o.superpose(x[None], t[None])
+        # msd = (sum |x'|^2 + sum |t'|^2 - 2 lambda) / N cancels to about 1e-15 of its terms.
+        size = (np.sum((x - xb) ** 2) + np.sum((t - tb) ** 2)) / len(x)
+        assert abs(got[12] - msd[0]) <= 1e-10 * msd[0] + 1e-14 * size
+        if unique and msd[0] > 1e-10 * size:
+            M = got[:9].reshape(3, 3)
+            assert np.abs(M - R[0].T).max() <= 1e-9
+            assert np.abs(got[9:12] - (xb[0] - R[0].T @ tb[0])).max() <= 1e-9 * max(1.0, np.abs(xb).max())
+
+
+def test_checks_catch_a_transposed_superposition(monkeypatch):
+    """Planted mistake: the rotation transposed in superposed_grad_xyz's superposition.  The
+    finite-difference pin above fails on it."""
+    real = o.superpose
+
+    def transposed(x, t):
+        R, xb, tb, msd = real(x, t)
+        return np.swapaxes(R, 1, 2), xb, tb, msd
+
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(1, 15, 3))
+    t = rng.normal(size=(1, 15, 3))
+    monkeypatch.setattr(o, "superpose", transposed)
+    g = o.superposed_grad_xyz(x, t, None, True)
+    monkeypatch.setattr(o, "superpose", real)
+    h = 1e-6
+    xp, xm = x.copy(), x.copy()
+    xp[0, 7, 2] += h
+    xm[0, 7, 2] -= h
+    fd = (o.superposed_loss(xp, t, True)[0] - o.superposed_loss(xm, t, True)[0]) / (2 * h)
+    assert abs(fd - g[0, 7, 2]) > 1e-4 * max(1.0, abs(fd))
