@@ -321,14 +321,15 @@ Tensor apply_anchored(const Tensor& lengths, const Tensor& angles, const Tensor&
 class LossAutograd : public torch::autograd::Function<LossAutograd> {
  public:
   static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
-                        Tensor target, Tensor p0, Tensor first_direction, Tensor initial_normal) {
+                        Tensor target, Tensor p0, Tensor first_direction, Tensor initial_normal, bool anchored) {
     const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true, anchored);
     check_like(target, lengths, "target", true);
     TORCH_CHECK(target.sizes() == torch::IntArrayRef({shape.batch, shape.points, 3}), "target must have shape (B, N, 3)");
     TORCH_CHECK(!target.requires_grad(), "target gradients are not supported");
     const c10::DeviceGuard guard(lengths.device());
     check_max_local_transforms(shape.points - 3, max_steps(lengths, CUFK_FORWARD), "reconstruct");
+    ctx->saved_data["anchored"] = anchored;
     Tensor loss = torch::empty({shape.batch}, lengths.options());
     Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
     Tensor regular = torch::empty({shape.batch}, lengths.options().dtype(torch::kUInt8));
@@ -353,7 +354,8 @@ class LossAutograd : public torch::autograd::Function<LossAutograd> {
     const Tensor& dihedrals = saved[2];
     const Tensor& target = saved[3];
     const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true);
+    const bool anchored = ctx->saved_data["anchored"].toBool();
+    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true, anchored);
     Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_loss, lengths, "grad_loss", true);
     const c10::DeviceGuard guard(lengths.device());
@@ -362,6 +364,21 @@ class LossAutograd : public torch::autograd::Function<LossAutograd> {
     Tensor grad_dihedrals = torch::empty_like(dihedrals);
     const Tensor xyz = ctx->saved_data["xyz"].toTensor();
     const Tensor regular = ctx->saved_data["regular"].toTensor();
+    if (anchored) {
+      Tensor grad_p0 = torch::empty({3}, lengths.options());
+      Tensor grad_fd = torch::empty({3}, lengths.options());
+      Tensor grad_n0 = torch::empty({3}, lengths.options());
+      Tensor work = torch::empty({std::max<int64_t>(shape.batch, 1) * 6}, lengths.options().dtype(torch::kFloat64));
+      check_status(cufk_reconstruct_loss_bwd_anchored(
+                       dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
+                       a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(), xyz.data_ptr(),
+                       static_cast<const uint8_t*>(regular.data_ptr()), target.data_ptr(), grad_loss.data_ptr(),
+                       grad_lengths.data_ptr(), grad_angles.data_ptr(), grad_dihedrals.data_ptr(),
+                       static_cast<double*>(work.data_ptr()), grad_p0.data_ptr(), grad_fd.data_ptr(),
+                       grad_n0.data_ptr(), shape.batch, shape.points, current_stream(lengths)),
+                   "cufk_reconstruct_loss_bwd_anchored");
+      return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), grad_p0, grad_fd, grad_n0, Tensor()};
+    }
     check_status(cufk_reconstruct_loss_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
                                            dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
                                            a.initial_normal.data_ptr(), xyz.data_ptr(),
@@ -370,13 +387,13 @@ class LossAutograd : public torch::autograd::Function<LossAutograd> {
                                            grad_lengths.data_ptr(), grad_angles.data_ptr(), grad_dihedrals.data_ptr(),
                                            shape.batch, shape.points, current_stream(lengths)),
                  "cufk_reconstruct_loss_bwd");
-    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
 
 Tensor apply_loss(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& target,
-                  const Tensor& p0, const Tensor& first_direction, const Tensor& initial_normal) {
-  return LossAutograd::apply(lengths, angles, dihedrals, target, p0, first_direction, initial_normal);
+                  const Tensor& p0, const Tensor& first_direction, const Tensor& initial_normal, bool anchor_grads) {
+  return LossAutograd::apply(lengths, angles, dihedrals, target, p0, first_direction, initial_normal, anchor_grads);
 }
 
 // ------------------------------------------------------------------ fused superposed loss
@@ -480,9 +497,11 @@ void long_forward(const Tensor& lengths, const Tensor& angles, const Tensor& dih
 class LongReconstructAutograd : public torch::autograd::Function<LongReconstructAutograd> {
  public:
   static Tensor forward(torch::autograd::AutogradContext* ctx, Tensor lengths, Tensor angles, Tensor dihedrals,
-                        Tensor p0, Tensor first_direction, Tensor initial_normal, int64_t segment_steps) {
+                        Tensor p0, Tensor first_direction, Tensor initial_normal, int64_t segment_steps,
+                        bool anchored) {
     const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true);
+    const Anchors a = checked_anchors(p0, first_direction, initial_normal, lengths, true, anchored);
+    ctx->saved_data["anchored"] = anchored;
     const c10::DeviceGuard guard(lengths.device());
     const int64_t seg = long_segment_steps(shape, segment_steps);
     Tensor xyz = torch::empty({shape.batch, shape.points, 3}, lengths.options());
@@ -507,7 +526,8 @@ class LongReconstructAutograd : public torch::autograd::Function<LongReconstruct
     Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_points, lengths, "grad_points", true);
     const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true);
+    const bool anchored = ctx->saved_data["anchored"].toBool();
+    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true, anchored);
     const c10::DeviceGuard guard(lengths.device());
     const int64_t seg = ctx->saved_data["segment_steps"].toInt();
     Tensor xyz = ctx->saved_data["xyz"].toTensor();
@@ -521,6 +541,23 @@ class LongReconstructAutograd : public torch::autograd::Function<LongReconstruct
     Tensor grad_lengths = torch::empty_like(lengths);
     Tensor grad_angles = torch::empty_like(angles);
     Tensor grad_dihedrals = torch::empty_like(dihedrals);
+    if (anchored) {
+      Tensor grad_p0 = torch::empty({3}, lengths.options());
+      Tensor grad_fd = torch::empty({3}, lengths.options());
+      Tensor grad_n0 = torch::empty({3}, lengths.options());
+      Tensor anchor_work =
+          torch::empty({std::max<int64_t>(shape.batch, 1) * 6}, lengths.options().dtype(torch::kFloat64));
+      check_status(cufk_reconstruct_long_bwd_anchored(
+                       dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(), dihedrals.data_ptr(),
+                       a.p0.data_ptr(), a.first_direction.data_ptr(), a.initial_normal.data_ptr(), xyz.data_ptr(),
+                       static_cast<const double*>(state.data_ptr()), grad_points.data_ptr(),
+                       static_cast<double*>(work.data_ptr()), grad_lengths.data_ptr(), grad_angles.data_ptr(),
+                       grad_dihedrals.data_ptr(), static_cast<double*>(anchor_work.data_ptr()), grad_p0.data_ptr(),
+                       grad_fd.data_ptr(), grad_n0.data_ptr(), shape.batch, shape.points, seg,
+                       current_stream(lengths)),
+                   "cufk_reconstruct_long_bwd_anchored");
+      return {grad_lengths, grad_angles, grad_dihedrals, grad_p0, grad_fd, grad_n0, Tensor(), Tensor()};
+    }
     check_status(cufk_reconstruct_long_bwd(dtype_code(lengths), lengths.data_ptr(), angles.data_ptr(),
                                            dihedrals.data_ptr(), a.p0.data_ptr(), a.first_direction.data_ptr(),
                                            a.initial_normal.data_ptr(), xyz.data_ptr(),
@@ -529,14 +566,15 @@ class LongReconstructAutograd : public torch::autograd::Function<LongReconstruct
                                            grad_angles.data_ptr(), grad_dihedrals.data_ptr(), shape.batch,
                                            shape.points, seg, current_stream(lengths)),
                  "cufk_reconstruct_long_bwd");
-    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor()};
+    return {grad_lengths, grad_angles, grad_dihedrals, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
 
 Tensor apply_reconstruct_long(const Tensor& lengths, const Tensor& angles, const Tensor& dihedrals, const Tensor& p0,
-                              const Tensor& first_direction, const Tensor& initial_normal, int64_t segment_steps) {
+                              const Tensor& first_direction, const Tensor& initial_normal, int64_t segment_steps,
+                              bool anchor_grads) {
   return LongReconstructAutograd::apply(lengths, angles, dihedrals, p0, first_direction, initial_normal,
-                                        segment_steps);
+                                        segment_steps, anchor_grads);
 }
 
 // ------------------------------------------------------------------ torsion
@@ -700,13 +738,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"));
   m.def("apply_loss", &apply_loss, "fused reconstruct + per-chain coordinate loss", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"), py::arg("first_direction"),
-        py::arg("initial_normal"));
+        py::arg("initial_normal"), py::arg("anchor_grads") = false);
   m.def("apply_superposed", &apply_superposed, "fused reconstruct + per-chain superposed loss (1 msd, 2 rmsd)",
         py::arg("lengths"), py::arg("angles"), py::arg("dihedrals"), py::arg("target"), py::arg("p0"),
         py::arg("first_direction"), py::arg("initial_normal"), py::arg("kind"));
   m.def("apply_long", &apply_reconstruct_long, "segmented reconstruct for chains of any length", py::arg("lengths"),
         py::arg("angles"), py::arg("dihedrals"), py::arg("p0"), py::arg("first_direction"), py::arg("initial_normal"),
-        py::arg("segment_steps") = 0);
+        py::arg("segment_steps") = 0, py::arg("anchor_grads") = false);
   m.def("long_segment_steps", [](int64_t batch, int64_t points) { return cufk_long_segment_steps(batch, points); });
   py::class_<TorsionModule>(m, "TorsionModule")
       .def(py::init<const std::vector<double>&, const std::vector<double>&, const std::vector<double>&>(),

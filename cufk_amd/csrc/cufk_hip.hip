@@ -357,6 +357,35 @@ int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles
   });
 }
 
+int cufk_reconstruct_loss_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                       const void* p0, const void* first_direction, const void* initial_normal,
+                                       const void* xyz, const uint8_t* chain_regular, const void* target,
+                                       const void* grad_loss, void* grad_lengths, void* grad_angles,
+                                       void* grad_dihedrals, double* anchor_work, void* grad_p0,
+                                       void* grad_first_direction, void* grad_initial_normal, int64_t batch,
+                                       int64_t points, void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_chain(batch, points);
+  if (rc != CUFK_OK) return rc;
+  if (!p0 || !first_direction || !initial_normal || !grad_p0 || !grad_first_direction || !grad_initial_normal)
+    return CUFK_ERR_NULL;
+  if (batch > 0 && (!lengths || !angles || !dihedrals || !xyz || !chain_regular || !target || !grad_lengths ||
+                    !grad_angles || !grad_dihedrals || !anchor_work))
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    if (batch > 0) {
+      const int r = loss_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                      cp<T>(first_direction), cp<T>(initial_normal), cp<T>(xyz), chain_regular,
+                                      cp<T>(target), cp<T>(grad_loss), mp<T>(grad_lengths), mp<T>(grad_angles),
+                                      mp<T>(grad_dihedrals), batch, static_cast<int>(points), st, anchor_work);
+      if (r != CUFK_OK) return r;
+    }
+    return anchor_grads_typed<T>(anchor_work, batch, cp<T>(first_direction), cp<T>(initial_normal), mp<T>(grad_p0),
+                                 mp<T>(grad_first_direction), mp<T>(grad_initial_normal), st);
+  });
+}
+
 int cufk_reconstruct_superposed_fwd(int dtype, int loss_kind, const void* lengths, const void* angles,
                                     const void* dihedrals, const void* p0, const void* first_direction,
                                     const void* initial_normal, const void* target, void* xyz, uint8_t* chain_regular,
@@ -498,6 +527,36 @@ int cufk_reconstruct_long_bwd(int dtype, const void* lengths, const void* angles
                              cp<T>(initial_normal), cp<T>(xyz), state, cp<T>(grad_xyz), work, mp<T>(grad_lengths),
                              mp<T>(grad_angles), mp<T>(grad_dihedrals), batch, static_cast<int>(points),
                              static_cast<int>(segment_steps), st);
+  });
+}
+
+int cufk_reconstruct_long_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                       const void* p0, const void* first_direction, const void* initial_normal,
+                                       const void* xyz, const double* state, const void* grad_xyz, double* work,
+                                       void* grad_lengths, void* grad_angles, void* grad_dihedrals,
+                                       double* anchor_work, void* grad_p0, void* grad_first_direction,
+                                       void* grad_initial_normal, int64_t batch, int64_t points, int64_t segment_steps,
+                                       void* stream) {
+  if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
+  const int rc = check_long(batch, points, segment_steps);
+  if (rc != CUFK_OK) return rc;
+  if (!p0 || !first_direction || !initial_normal || !grad_p0 || !grad_first_direction || !grad_initial_normal)
+    return CUFK_ERR_NULL;
+  if (batch > 0 && (!lengths || !angles || !dihedrals || !xyz || !state || !grad_xyz || !work || !grad_lengths ||
+                    !grad_angles || !grad_dihedrals || !anchor_work))
+    return CUFK_ERR_NULL;
+  auto st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, [&]<typename T>() {
+    if (batch > 0) {
+      const int r = long_bwd_typed<T>(cp<T>(lengths), cp<T>(angles), cp<T>(dihedrals), cp<T>(p0),
+                                      cp<T>(first_direction), cp<T>(initial_normal), cp<T>(xyz), state,
+                                      cp<T>(grad_xyz), work, mp<T>(grad_lengths), mp<T>(grad_angles),
+                                      mp<T>(grad_dihedrals), batch, static_cast<int>(points),
+                                      static_cast<int>(segment_steps), st, anchor_work);
+      if (r != CUFK_OK) return r;
+    }
+    return anchor_grads_typed<T>(anchor_work, batch, cp<T>(first_direction), cp<T>(initial_normal), mp<T>(grad_p0),
+                                 mp<T>(grad_first_direction), mp<T>(grad_initial_normal), st);
   });
 }
 

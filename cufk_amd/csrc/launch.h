@@ -109,7 +109,7 @@ int loss_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
 template <typename T>
 int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
                    const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
-                   hipStream_t st);
+                   hipStream_t st, double* anchor = nullptr);
 
 // Fused superposed losses (mean squared deviation after optimal superposition, or its
 // square root unless `squared`); record: kSuperposeRecord doubles per chain (superpose.h).
@@ -129,7 +129,7 @@ int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
 template <typename T>
 int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
                    const double* state, const T* g, double* work, T* gL, T* gA, T* gD, int64_t B, int N, int S,
-                   hipStream_t st);
+                   hipStream_t st, double* anchor = nullptr);
 
 // Torsion path.
 template <typename T>

@@ -64,11 +64,25 @@ namespace cufk_amd {
 // on too few items).  The exact backward uses the same plans.  The kernels stage rows with one
 // word of padding per lane: at (4, 8) that lets five forward workgroups (three backward)
 // share a CU instead of four (two).
+//
+// Small grids (`groups` workgroups of one chain each, at most kLatencyWaves waves under the
+// eight-item plan, four per SIMD) run latency-bound: a lone wave per SIMD waits on every
+// dependent instruction.  There the chain takes twice the waves with four items per lane,
+// halving each lane's serial scan.  Measured on MI355X (forward + position-based backward,
+// back-to-back launches): B=1024, N=384: 13.6 against 15.1 us; B=512, N=384: 11.4 against
+// 12.5 us; B=2048, N=700: 30.1 against 33.2 us.
 constexpr int kScanPad = 1;
-template <typename Fn> int with_scan_plan(int steps, Fn&& fn) {
+constexpr int64_t kLatencyWaves = 4096;
+template <typename Fn> int with_scan_plan(int64_t groups, int steps, Fn&& fn) {
   if (steps <= 256) return fn.template operator()<1, 4>();
-  if (steps <= 512) return fn.template operator()<1, 8>();
-  if (steps <= 1024) return fn.template operator()<2, 8>();
+  if (steps <= 512) {
+    if (groups <= kLatencyWaves) return fn.template operator()<2, 4>();
+    return fn.template operator()<1, 8>();
+  }
+  if (steps <= 1024) {
+    if (2 * groups <= kLatencyWaves) return fn.template operator()<4, 4>();
+    return fn.template operator()<2, 8>();
+  }
   return fn.template operator()<4, 8>();
 }
 
@@ -146,7 +160,7 @@ template <typename T>
 int reconstruct_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz,
                           uint8_t* regular, int64_t B, int N, hipStream_t st) {
   if (use_packed_fwd(B, N - 3)) return packed_fwd_typed<T>(L, A, D, p0, fd, n0, xyz, regular, B, N, st);
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st, L + off * (N - 1),
                          A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
@@ -159,7 +173,7 @@ template <typename T>
 int shadow_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, T* xyz, float* pos,
                      uint8_t* regular, int64_t B, int N, hipStream_t st) {
   if (!use_shadow(B, N - 3)) return reconstruct_fwd_typed<T>(L, A, D, p0, fd, n0, xyz, nullptr, B, N, st);
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_forward_shadow_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
@@ -185,7 +199,7 @@ int reconstruct_bwd_recompute_typed(const T* L, const T* A, const T* D, const T*
                                     double* anchor) {
   if (use_packed_bwd(B, N - 3))
     return packed_bwd_typed<T, false>(L, A, D, p0, fd, n0, nullptr, nullptr, g, gL, gA, gD, B, N, st, anchor);
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_recompute_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, g + off * N * 3,
@@ -209,7 +223,7 @@ int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0,
                                 hipStream_t st, double* anchor) {
   if (use_packed_bwd(B, N - 3))
     return packed_bwd_typed<T, true>(L, A, D, p0, fd, n0, xyz, regular, g, gL, gA, gD, B, N, st, anchor);
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
@@ -223,7 +237,7 @@ template <typename T>
 int shadow_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const float* pos,
                      const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
   if (!use_shadow(B, N - 3)) return reconstruct_bwd_recompute_typed<T>(L, A, D, p0, fd, n0, g, gL, gA, gD, B, N, st);
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad, float>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, pos + off * N * 3,
@@ -300,7 +314,7 @@ namespace cufk_amd {
 template <typename T>
 int loss_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target, T* xyz,
                    uint8_t* regular, T* loss, int64_t B, int N, hipStream_t st) {
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_loss_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, target + off * N * 3,
@@ -312,13 +326,14 @@ int loss_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
 template <typename T>
 int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
                    const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
-                   hipStream_t st) {
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+                   hipStream_t st, double* anchor) {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
                          regular + off, target + off * N * 3, grad_loss != nullptr ? grad_loss + off : nullptr,
-                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N);
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N, nullptr, 0,
+                         anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
 }
@@ -327,7 +342,7 @@ template <typename T>
 int superposed_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* target,
                          T* xyz, uint8_t* regular, T* loss, double* record, int squared, int64_t B, int N,
                          hipStream_t st) {
-  const int rc = with_scan_plan(N - 3, [&]<int W, int K>() {
+  const int rc = with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_superposed_forward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, target + off * N * 3,
@@ -342,7 +357,7 @@ template <typename T>
 int superposed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
                          const uint8_t* regular, const T* target, const double* record, const T* grad_loss,
                          int squared, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
-  return with_scan_plan(N - 3, [&]<int W, int K>() {
+  return with_scan_plan(B, N - 3, [&]<int W, int K>() {
     return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
       hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad, kLossSuperposed>), dim3(n), dim3(64 * W),
                          0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
@@ -371,7 +386,7 @@ int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
   const int segs = static_cast<int>(long_segments(N, S));
   uint8_t* const flags = reinterpret_cast<uint8_t*>(state + long_flag_offset(B, segs));
   T* const local = reinterpret_cast<T*>(state + long_local_offset(B, segs));
-  const int rc = with_scan_plan(S, [&]<int W, int K>() {
+  const int rc = with_scan_plan(B * segs, S, [&]<int W, int K>() {
     hipLaunchKernelGGL((long_forward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
                        dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, local, flags, state, N, S, segs);
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
@@ -389,7 +404,7 @@ int long_fwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
 template <typename T>
 int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd, const T* n0, const T* xyz,
                    const double* state, const T* g, double* work, T* gL, T* gA, T* gD, int64_t B, int N, int S,
-                   hipStream_t st) {
+                   hipStream_t st, double* anchor) {
   const int segs = static_cast<int>(long_segments(N, S));
   const uint8_t* const flags = reinterpret_cast<const uint8_t*>(state + long_flag_offset(B, segs));
   const T* const local = reinterpret_cast<const T*>(state + long_local_offset(B, segs));
@@ -400,10 +415,10 @@ int long_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
   hipLaunchKernelGGL(long_backward_carry_kernel, dim3(static_cast<unsigned>((B + kChainsPerGroup - 1) / kChainsPerGroup)),
                      dim3(kLongThreads), 0, st, state, work, B, segs);
   if (hipGetLastError() != hipSuccess) return CUFK_ERR_LAUNCH;
-  return with_scan_plan(S, [&]<int W, int K>() {
+  return with_scan_plan(B * segs, S, [&]<int W, int K>() {
     hipLaunchKernelGGL((long_backward_segments_kernel<T, W, K, kScanPad>), dim3(static_cast<unsigned>(B * segs)),
                        dim3(64 * W), 0, st, L, A, D, p0, fd, n0, xyz, local, flags, g, gL, gA, gD, state, work, N,
-                       S, segs);
+                       S, segs, anchor);
     return hipGetLastError() == hipSuccess ? CUFK_OK : CUFK_ERR_LAUNCH;
   });
 }

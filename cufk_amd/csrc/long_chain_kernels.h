@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
     const T* __restrict__ xyz, const T* __restrict__ local, const uint8_t* __restrict__ flags,
     const T* __restrict__ grad_xyz, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
     T* __restrict__ grad_dihedrals, const double* __restrict__ state, const double* __restrict__ work, int points,
-    int seg_steps, int segments) {
+    int seg_steps, int segments, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
@@ -280,6 +280,9 @@ __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
   const int64_t b = s.chain;
   const int64_t at = b * segments + s.index;
   const bool head = s.index == 0;
+  // The head segment's adjoint holds the whole chain's force and moment sums (its carry holds
+  // every later segment's): it writes the chain's anchor sums.
+  double* const an = head && anchor != nullptr ? anchor + b * 6 : nullptr;
   // Position-based adjoint where this segment and the one before it (which holds the bond
   // x1-x2) passed the forward's tests on their own positions.
   if (FastPath<T>::kEnabled && flags[at] != 0 && (head || flags[at - 1] != 0)) {
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
     __syncthreads();
     position_adjoint<T, Lay, true>(grad_lengths + b * (points - 1) + s.first, grad_angles + b * (points - 2) + s.first,
                                    grad_dihedrals + b * (points - 3) + s.first, pstage, gstage, wave_sum, s.steps + 3,
-                                   nullptr, head, state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6,
+                                   an, head, state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6,
                                    head ? R(0) : widen(lengths[b * (points - 1) + s.first + 1]));
     return;
   }
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(64 * W) void long_backward_segments_kernel(
                             grad_xyz + (b * points + s.first) * 3, grad_lengths + b * (points - 1) + s.first,
                             grad_angles + b * (points - 2) + s.first, grad_dihedrals + b * (points - 3) + s.first,
                             pstage, gstage, wave_total, wave_sum, wide_vote, s.steps + 3, s.index == 0,
-                            state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6);
+                            state + at * kLongStateDoubles + 12, work + at * kLongWorkDoubles + 6, an);
 }
 
 }  // namespace cufk_amd

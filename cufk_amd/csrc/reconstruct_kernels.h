@@ -187,7 +187,7 @@ __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const co
 // Shadow (float16/bfloat16 whole chains): the positions are also stored unrounded, in float,
 // to shadow (the chain's (points, 3) row), and *regular receives the float32 chains' test
 // (FastPath<float>) on them, for the position-based backward over that copy.
-template <typename T, typename Lay, bool Segmented, int LossKind = kLossNone, bool Shadow = false>
+template <typename T, typename Lay, bool Segmented, int LossKind = kLossNone, bool Shadow = false, bool Lat = false>
 __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                               const T* __restrict__ Dr, const T* __restrict__ p0,
                                               const T* __restrict__ first_direction,
@@ -226,7 +226,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
-  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, Lay::kLanes);
+  if constexpr (sizeof(R) == 4 && !Lat) sin_cos_table_init(sc_table, tid, Lay::kLanes);
   if constexpr (!Segmented) pad_lane_tail<K>(stage + b0, stage + Lay::kStepRow + b0, stage + 2 * Lay::kStepRow + b0, count);
   // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
@@ -246,14 +246,17 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     const R* const Ls = stage + b0;
     const R* const As = stage + Lay::kStepRow + b0;
     const R* const Ds = stage + 2 * Lay::kStepRow + b0;
-    constexpr bool kTable = sizeof(R) == 4;
+    // Lat (small batches, a wave or two per SIMD, where latency rather than issue bounds the
+    // scan): sin/cos from the polynomial, not the LDS table, and no scheduling barriers, so the
+    // compiler may overlap the items' loads and sin/cos.
+    constexpr bool kTable = sizeof(R) == 4 && !Lat;
     if constexpr (Segmented) {
       if (wide)
         lane_scan<T, K, true, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
       else
         lane_scan<T, K, false, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
-      lane_scan_chain<T, K, kTable, true, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
+      lane_scan_chain<T, K, kTable, !Lat, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
                                                 lmin);
     }
   }
@@ -374,13 +377,13 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   if constexpr (Shadow) store_point_row<Lay>(shadow, stage, points, tid);
 }
 
-template <typename T, int W, int K, int Pad = 4>
+template <typename T, int W, int K, int Pad = 4, bool Lat = false>
 __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
   const int64_t row = blockIdx.x;
-  forward_chain<T, Layout<W, K, Pad>, false>(lengths + row * (points - 1), angles + row * (points - 2),
+  forward_chain<T, Layout<W, K, Pad>, false, kLossNone, false, Lat>(lengths + row * (points - 1), angles + row * (points - 2),
                                              dihedrals + row * (points - 3), p0, first_direction, initial_normal,
                                              xyz + row * points * 3, regular != nullptr ? regular + row : nullptr,
                                              points, true, nullptr);
@@ -1058,14 +1061,16 @@ __global__ __launch_bounds__(64 * W) void reconstruct_superposed_forward_kernel(
 // position-based adjoint loads them for regular chains, in LDS before the exact adjoint for the
 // others.  kLossSquared: 2 w_b (x - target).  kLossSuperposed: c (x - M t - a) from the
 // chain's superposition record (superpose.h), c = (2/N) w_b, divided by 2 rmsd unless
-// `squared` (0 where rmsd = 0).
+// `squared` (0 where rmsd = 0).  With `anchor`, each chain also writes its six anchor sums
+// (store_anchor_sums) for anchor_gradients_kernel.
 template <typename T, int W, int K, int Pad, int LossKind = kLossSquared>
 __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ target,
     const T* __restrict__ grad_loss, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points, const double* __restrict__ record = nullptr, int squared = 0) {
+    T* __restrict__ grad_dihedrals, int points, const double* __restrict__ record = nullptr, int squared = 0,
+    double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   using Res = std::conditional_t<LossKind == kLossSuperposed, SuperposedResidual<R>, SquaredResidual<R>>;
@@ -1089,9 +1094,10 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
   T* gDr = grad_dihedrals + row * (points - 3);
+  double* const an = anchor != nullptr ? anchor + row * 6 : nullptr;
   if (FastPath<T>::kEnabled && regular[row] != 0) {
-    position_adjoint<T, Lay, false, Res>(gLr, gAr, gDr, region_a, region_b, wave_sum, points, nullptr, true, nullptr,
-                                         nullptr, R(0), res);
+    position_adjoint<T, Lay, false, Res>(gLr, gAr, gDr, region_a, region_b, wave_sum, points, an, true, nullptr, nullptr,
+                                         R(0), res);
   } else {
     for (int p = tid; p < points; p += Lay::kLanes) {
       const int slot = Lay::point_slot(3 * p);  // a point's three coordinates share a lane segment
@@ -1103,7 +1109,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
     __syncthreads();
     exact_chain<T, Lay, false, false>(lengths + row * (points - 1), angles + row * (points - 2),
                                       dihedrals + row * (points - 3), p0, first_direction, initial_normal, nullptr, gLr,
-                                      gAr, gDr, region_a, region_b, wave_total, wave_sum, wide_vote, points);
+                                      gAr, gDr, region_a, region_b, wave_total, wave_sum, wide_vote, points, true,
+                                      nullptr, nullptr, an);
   }
 }
 

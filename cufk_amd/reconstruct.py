@@ -89,20 +89,25 @@ def reconstruct_long(
     first_direction: torch.Tensor | None = None,
     initial_normal: torch.Tensor | None = None,
     segment_steps: int | None = None,
+    *,
+    anchor_grads: bool = False,
 ) -> torch.Tensor:
     r"""``reconstruct`` for chains of any length (N >= 4, no 2051-point cap).
 
-    Same arguments, defaults, validation and gradients as :func:`reconstruct`.  The chain is
-    cut into segments of ``segment_steps`` local transforms (1..2048; by default 2048, halved
-    down to 256 while fewer than 1024 segments would run), each reconstructed by one
-    workgroup and joined in float64; the backward applies the exact adjoint per segment.
-    Without ``segment_steps``, chains of at most 2051 points take :func:`reconstruct` itself.
+    Same arguments, defaults, validation and gradients as :func:`reconstruct` (including
+    ``anchor_grads``).  The chain is cut into segments of ``segment_steps`` local transforms
+    (1..2048; by default 2048, halved down to 256 while fewer than 1024 segments would run),
+    each reconstructed by one workgroup and joined in float64.  The backward takes, per
+    segment, the position-based adjoint over the segment's own local positions where the
+    forward's tests passed for it and for the segment before it, and the exact adjoint
+    elsewhere.  Without ``segment_steps``, chains of at most 2051 points take
+    :func:`reconstruct` itself.
 
     The reference has no counterpart (its README leaves long chains to a separate
     repository); this extends its interface rather than mirroring it.
     """
     if segment_steps is None and lengths.shape[-1] + 1 <= BLOCK_SCAN_MAX_POINT_COUNT:
-        return reconstruct(lengths, angles, dihedrals, p0, first_direction, initial_normal)
+        return reconstruct(lengths, angles, dihedrals, p0, first_direction, initial_normal, anchor_grads=anchor_grads)
     lengths, angles, dihedrals, single = _batched_inputs(lengths, angles, dihedrals)
     p0 = _anchor(p0, (0.0, 0.0, 0.0), lengths)
     first_direction = _anchor(first_direction, (1.0, 0.0, 0.0), lengths)
@@ -115,6 +120,7 @@ def reconstruct_long(
         first_direction,
         initial_normal,
         0 if segment_steps is None else int(segment_steps),
+        anchor_grads,
     )
     return xyz[0] if single else xyz
 
@@ -127,6 +133,8 @@ def reconstruct_loss(
     p0: torch.Tensor | None = None,
     first_direction: torch.Tensor | None = None,
     initial_normal: torch.Tensor | None = None,
+    *,
+    anchor_grads: bool = False,
 ) -> torch.Tensor:
     r"""Per-chain coordinate loss :math:`\sum_i \lVert x_i - t_i \rVert^2` of the reconstruction,
     fused with it.
@@ -140,6 +148,8 @@ def reconstruct_loss(
         lengths, angles, dihedrals, p0, first_direction, initial_normal: as for
             :func:`reconstruct` (4 <= N <= 2051).
         target: ``(N, 3)`` or ``(B, N, 3)``, dtype and device of ``lengths``; no gradient.
+        anchor_grads: as for :func:`reconstruct`: the anchors may require grad and receive
+            gradients.
 
     Returns:
         ``(B,)`` losses, or a 0-d tensor for one chain.  Gradients flow to lengths, angles and
@@ -159,6 +169,7 @@ def reconstruct_loss(
         p0,
         first_direction,
         initial_normal,
+        anchor_grads,
     )
     return loss[0] if single else loss
 

@@ -226,6 +226,19 @@ int cufk_reconstruct_loss_bwd(int dtype, const void* lengths, const void* angles
                               int64_t points, void* stream);
 
 /*
+ * cufk_reconstruct_loss_bwd plus the anchors' gradients (summed over the batch), as
+ * cufk_reconstruct_bwd_anchored adds them to the backward of reconstruct; anchor_work: 6*B
+ * doubles of scratch.  No reference counterpart (extension_utils.cuh:81 rejects anchor grads).
+ */
+int cufk_reconstruct_loss_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                       const void* p0, const void* first_direction, const void* initial_normal,
+                                       const void* xyz, const uint8_t* chain_regular, const void* target,
+                                       const void* grad_loss, void* grad_lengths, void* grad_angles,
+                                       void* grad_dihedrals, double* anchor_work, void* grad_p0,
+                                       void* grad_first_direction, void* grad_initial_normal, int64_t batch,
+                                       int64_t points, void* stream);
+
+/*
  * Fused superposed losses: loss[b] = min over rotations R of (1/N) sum_i |R (x_i - xbar) -
  * (t_i - tbar)|^2 (CUFK_LOSS_MSD), or its square root (CUFK_LOSS_RMSD), x the reconstruction of
  * (lengths, angles, dihedrals, anchors) as stored (rounded to the dtype) and t = target (B, N, 3).
@@ -295,6 +308,19 @@ int cufk_reconstruct_long_bwd(int dtype, const void* lengths, const void* angles
                               const double* state, const void* grad_xyz, double* work, void* grad_lengths,
                               void* grad_angles, void* grad_dihedrals, int64_t batch, int64_t points,
                               int64_t segment_steps, void* stream);
+
+/*
+ * cufk_reconstruct_long_bwd plus the anchors' gradients (summed over the batch); anchor_work:
+ * 6*B doubles of scratch.  The head segment's adjoint holds each chain's whole force and moment
+ * sums and writes them.  No reference counterpart.
+ */
+int cufk_reconstruct_long_bwd_anchored(int dtype, const void* lengths, const void* angles, const void* dihedrals,
+                                       const void* p0, const void* first_direction, const void* initial_normal,
+                                       const void* xyz, const double* state, const void* grad_xyz, double* work,
+                                       void* grad_lengths, void* grad_angles, void* grad_dihedrals,
+                                       double* anchor_work, void* grad_p0, void* grad_first_direction,
+                                       void* grad_initial_normal, int64_t batch, int64_t points, int64_t segment_steps,
+                                       void* stream);
 
 /*
  * Largest step count (N-3) accepted for (dtype, direction) on `device`, or a negative

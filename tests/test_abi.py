@@ -72,8 +72,10 @@ def test_header_declares_the_entry_points():
         "cufk_reconstruct_fwd_flagged",
         "cufk_reconstruct_fwd_shadow",
         "cufk_reconstruct_long_bwd",
+        "cufk_reconstruct_long_bwd_anchored",
         "cufk_reconstruct_long_fwd",
         "cufk_reconstruct_loss_bwd",
+        "cufk_reconstruct_loss_bwd_anchored",
         "cufk_reconstruct_loss_fwd",
         "cufk_reconstruct_shadow_floats",
         "cufk_reconstruct_superposed_bwd",

@@ -107,3 +107,78 @@ def test_plain_reconstruct_still_rejects_anchor_grads(cufk, device):
     L, A, D = torch.ones(1, 9, device=device), torch.ones(1, 8, device=device), torch.ones(1, 7, device=device)
     with pytest.raises(RuntimeError, match="p0 gradients are not supported"):
         cufk.reconstruct(L, A, D, torch.zeros(3, device=device, requires_grad=True))
+
+
+# ----------------------------------------------------------------- fused coordinate loss, long chains
+
+
+def _loss_case(B, N, seed, dtype=torch.float64):
+    d = _case(B, N, seed, dtype)
+    an = {k: d[k] for k in ("p0", "first_direction", "initial_normal")}
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **an)
+    d["target"] = _round(x + np.random.default_rng(seed).normal(0.0, 0.3, x.shape), dtype)
+    return d
+
+
+@pytest.mark.parametrize("B,N", [(3, 5), (3, 300), (2, 2051)])
+def test_anchor_gradients_fused_loss_fp64(cufk, device, B, N):
+    """reconstruct_loss(..., anchor_grads=True): the oracle's anchor map applied to the loss's
+    grad_xyz = 2 w (x - t), per-chain weights; every output within 1e-10."""
+    d = _loss_case(B, N, seed=900 + N)
+    w = np.linspace(0.5, 2.0, B)
+    L, A, D = (_dev(d[k], torch.float64, device, True) for k in ("lengths", "angles", "dihedrals"))
+    an = [_dev(d[k], torch.float64, device, True) for k in ("p0", "first_direction", "initial_normal")]
+    loss = cufk.reconstruct_loss(L, A, D, _dev(d["target"], torch.float64, device), *an, anchor_grads=True)
+    got = torch.autograd.grad(loss, (L, A, D, *an), _dev(w, torch.float64, device))
+    a = {k: d[k] for k in ("p0", "first_direction", "initial_normal")}
+    x = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **a)
+    gx = 2.0 * w[:, None, None] * (x - d["target"])
+    want = list(o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], gx, **a))
+    want += list(o.anchor_gradients(d["lengths"], d["angles"], d["dihedrals"], gx, **a))
+    for name, g, r in zip(("L", "A", "D", "p0", "fd", "n0"), got, want):
+        err = np.abs(g.cpu().numpy() - r).max() / max(np.abs(r).max(), 1e-300)
+        assert err <= 1e-10, (name, err)
+
+
+def test_anchor_gradients_fused_loss_gradcheck(cufk, device):
+    d = _loss_case(2, 12, seed=17)
+    L, A, D = (_dev(d[k], torch.float64, device) for k in ("lengths", "angles", "dihedrals"))
+    t = _dev(d["target"], torch.float64, device)
+    an = tuple(_dev(d[k], torch.float64, device, True) for k in ("p0", "first_direction", "initial_normal"))
+    assert torch.autograd.gradcheck(lambda p, f, n: cufk.reconstruct_loss(L, A, D, t, p, f, n, anchor_grads=True), an,
+                                    eps=1e-6, atol=1e-7, rtol=1e-6)
+
+
+@pytest.mark.parametrize("N,seg", [(300, 64), (700, 100), (2051, None)])
+@pytest.mark.parametrize("modify", [False, True])
+def test_anchor_gradients_long_chains_fp64(cufk, device, N, seg, modify):
+    """reconstruct_long(..., anchor_grads=True) over several segments (the head segment writes
+    the chain's sums), with the saved output and after an in-place change; within 1e-10."""
+    d = _case(3, N, seed=950 + N)
+    L, A, D = (_dev(d[k], torch.float64, device, True) for k in ("lengths", "angles", "dihedrals"))
+    an = [_dev(d[k], torch.float64, device, True) for k in ("p0", "first_direction", "initial_normal")]
+    xyz = cufk.reconstruct_long(L, A, D, *an, segment_steps=seg, anchor_grads=True)
+    if modify:
+        xyz.mul_(1.0)
+    got = torch.autograd.grad(xyz, (L, A, D, *an), _dev(d["grad"], torch.float64, device))
+    for name, g, r in zip(("L", "A", "D", "p0", "fd", "n0"), got, _ref(d)):
+        err = np.abs(g.cpu().numpy() - r).max() / max(np.abs(r).max(), 1e-300)
+        assert err <= 1e-10, (name, err)
+
+
+def test_anchor_gradients_long_chains_fp32_and_gradcheck(cufk, device):
+    d = _case(4, 3000, seed=31, dtype=torch.float32)
+    L, A, D = (_dev(d[k], torch.float32, device, True) for k in ("lengths", "angles", "dihedrals"))
+    an = [_dev(d[k], torch.float32, device, True) for k in ("p0", "first_direction", "initial_normal")]
+    xyz = cufk.reconstruct_long(L, A, D, *an, segment_steps=512, anchor_grads=True)
+    got = torch.autograd.grad(xyz, (L, A, D, *an), _dev(d["grad"], torch.float32, device))
+    for name, g, r in list(zip(("L", "A", "D", "p0", "fd", "n0"), got, _ref(d)))[3:]:
+        err = np.abs(g.double().cpu().numpy() - r).max() / np.abs(r).max()
+        print(f"fp32 long anchor {name}: rel err {err:.2e}")
+        assert err <= 5e-5, name
+    e = _case(2, 23, seed=33)
+    L, A, D = (_dev(e[k], torch.float64, device) for k in ("lengths", "angles", "dihedrals"))
+    an = tuple(_dev(e[k], torch.float64, device, True) for k in ("p0", "first_direction", "initial_normal"))
+    assert torch.autograd.gradcheck(
+        lambda p, f, n: cufk.reconstruct_long(L, A, D, p, f, n, segment_steps=4, anchor_grads=True), an, eps=1e-6,
+        atol=1e-7, rtol=1e-6)

@@ -226,3 +226,58 @@ def test_packed_unaligned_storage(lib, device, dtype):
         outs.append([t.clone() for t in (xyz, gL, gA, gD)])
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+# ----------------------------------------------------------------- plans chosen by batch and length
+#
+# One chain per workgroup for 257..1024 steps takes two plans, picked by the grid's size: small
+# grids (at most 4096 waves under the eight-item plan) take twice the waves at four items per
+# lane, larger grids eight items per lane.  Each (batch, length) below sits on one side of that
+# line, at a plan edge.
+
+
+_PLAN_CASES = {}
+
+
+def _plan_case(B, N):
+    """Inputs and the oracle's forward and gradients, computed once per shape."""
+    if (B, N) not in _PLAN_CASES:
+        d = _inputs(B, N, seed=600 + N + B)
+        ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+        ref_g = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+        _PLAN_CASES.clear()
+        _PLAN_CASES[(B, N)] = (d, ref, ref_g)
+    return _PLAN_CASES[(B, N)]
+
+
+@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("B,N", [(1024, 260), (1024, 384), (1024, 515), (4097, 260), (4097, 515),
+                                 (1024, 516), (1024, 700), (2048, 1027), (2049, 516), (2049, 1027)])
+def test_plans_by_batch_fp64(lib, device, B, N, recompute):
+    """float64 forward within 1e-12 and gradients within 1e-10 of the oracle on every chain."""
+    d, ref, ref_g = _plan_case(B, N)
+    xyz, reg, grads = _abi_run(lib, d, torch.float64, device, recompute)
+    assert np.abs(xyz.cpu().numpy() - ref).max() <= 1e-12 * max(1.0, np.abs(ref).max())
+    assert reg.cpu().min() == 1
+    for got, want in zip(grads, ref_g):
+        assert np.abs(got.cpu().numpy() - want).max() <= 1e-10 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("B,N", [(1024, 384), (4097, 384), (1024, 1027), (2049, 1027)])
+def test_plans_by_batch_fp32(cufk, device, B, N):
+    """float32 through the autograd path: 1e-5 nm RMS and 1e-4 nm max forward, gradients 5e-5
+    relative (normwise per chain)."""
+    d = _inputs(B, N, seed=650 + N, dtype=torch.float32)
+    L, A, D = (_dev(d[k], torch.float32, device, True) for k in ("lengths", "angles", "dihedrals"))
+    an = {k: _dev(d[k], torch.float32, device) for k in ("p0", "first_direction", "initial_normal")}
+    xyz = cufk.reconstruct(L, A, D, **an)
+    grads = torch.autograd.grad(xyz, (L, A, D), _dev(d["grad"], torch.float32, device))
+    ref = o.reconstruct_forward(d["lengths"], d["angles"], d["dihedrals"], **_anchor_np(d))
+    diff = xyz.detach().double().cpu().numpy() - ref
+    rms = math.sqrt(np.mean(np.sum(diff**2, axis=-1)))
+    print(f"fp32 B={B} N={N}: rms {rms:.3e} nm, max {np.abs(diff).max():.3e} nm")
+    assert rms <= 1e-5 and np.abs(diff).max() <= 1e-4
+    ref_g = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"], **_anchor_np(d))
+    for got, want in zip(grads, ref_g):
+        gerr = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
+        assert gerr.max() <= 5e-5, gerr.max()
