@@ -417,7 +417,7 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
         bool reg = all_ok && ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= FastPath<T>::kSinMin;
         const R mm = fmin(m, fmin(ff.L0, ff.L1));
         const R x = fmax(xm, abs_max3(abs_max3(abs_max3(R(0), ff.p0), ff.p1), ff.p2));
-        reg = reg && x <= static_cast<R>(FastPath<T>::kScale) * mm && mm >= static_cast<R>(FastPath<T>::kMinLength);
+        reg = reg && fast_extent_ok<FastPath<T>>(x, mm);
         regular[b0 + ln.c] = reg ? 1 : 0;
       }
     }
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
       const bool reg = all_ok && ff.L0 > R(0) && ff.L1 > R(0) && ff.sinA0 >= static_cast<R>(Fast::kSinMin);
       const R mm = fmin(m, fmin(ff.L0, ff.L1));
       const R xx = fmax(xm, abs_max3(abs_max3(R(0), a), bb));
-      irregular = !(reg && xx <= static_cast<R>(Fast::kScale) * mm && mm >= static_cast<R>(Fast::kMinLength));
+      irregular = !(reg && fast_extent_ok<Fast>(xx, mm));
     }
     positions = !block_any<W>(irregular, vote, lane, wave);  // barrier: parameter reads retired
     if (positions) {

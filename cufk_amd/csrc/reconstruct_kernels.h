@@ -27,27 +27,38 @@ namespace cufk_amd {
 // with sin >= kSinMin, and every coordinate within kScale shortest bonds of the origin (the
 // stored positions then resolve bond directions to about kScale ulp / bond).  The shortest
 // bond is also at least kMinLength, which keeps every squared bond length and squared bond
-// normal that the adjoint normalises far from the denormal range (rsqrt_bond).  float16/bfloat16
-// outputs are too coarse for it; their float copy (reconstruct_forward_shadow_kernel) takes
-// the float test.
+// normal that the adjoint normalises far from the denormal range (rsqrt_bond), and every
+// coordinate at most kMaxExtent, which keeps them below the largest finite value (bonds are
+// then at most 2 sqrt(3) kMaxExtent long).  float16/bfloat16 outputs are too coarse for it;
+// their float copy (reconstruct_forward_shadow_kernel) takes the float test.
 template <typename T> struct FastPath {
   static constexpr bool kEnabled = false;
   static constexpr double kSinMin = 2.0;
   static constexpr double kScale = 0.0;
   static constexpr double kMinLength = 0.0;
+  static constexpr double kMaxExtent = 0.0;
 };
 template <> struct FastPath<float> {
   static constexpr bool kEnabled = true;
   static constexpr double kSinMin = 0.5;
   static constexpr double kScale = 256.0;
   static constexpr double kMinLength = 0x1p-20;  // |b|^2 >= 2^-40, |b1 x b2|^2 >= 2^-82
+  static constexpr double kMaxExtent = 0x1p29;   // |b|^2 <= 12 * 2^58, |b1 x b2|^2 <= 2^123.2 < FLT_MAX
 };
 template <> struct FastPath<double> {
   static constexpr bool kEnabled = true;
   static constexpr double kSinMin = 1.0e-2;
   static constexpr double kScale = 8192.0;
   static constexpr double kMinLength = 0.0;  // the double adjoint keeps the library rsqrt
+  static constexpr double kMaxExtent = 0x1p250;
 };
+
+// The extent tests of the fast path for a chain with largest |coordinate| xmax and shortest
+// bond lmin (the bond and angle tests are separate).
+template <typename Fast, typename R> __device__ __forceinline__ bool fast_extent_ok(R xmax, R lmin) {
+  return xmax <= static_cast<R>(Fast::kScale) * lmin && lmin >= static_cast<R>(Fast::kMinLength) &&
+         xmax <= static_cast<R>(Fast::kMaxExtent);
+}
 
 template <typename R> __device__ __forceinline__ R abs_max3(R m, V3<R> x) {
   m = fmax(m, fabs(x.x));
@@ -368,7 +379,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
         m = fmin(m, wave_stat[w][1]);
         x = fmax(x, wave_stat[w][2]);
       }
-      reg = reg && x <= static_cast<R>(Fast::kScale) * m && m >= static_cast<R>(Fast::kMinLength);
+      reg = reg && fast_extent_ok<Fast>(x, m);
     }
     *regular = reg ? 1 : 0;
   }
@@ -867,7 +878,7 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
       m = fmin(m, wave_stat[w][1]);
       xm = fmax(xm, wave_stat[w][2]);
     }
-    regular = regular && xm <= static_cast<R>(Fast::kScale) * m && m >= static_cast<R>(Fast::kMinLength);
+    regular = regular && fast_extent_ok<Fast>(xm, m);
   }
   if (regular) {
     const int o0 = Lay::lane_point_base(tid);

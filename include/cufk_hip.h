@@ -88,7 +88,8 @@ int cufk_reconstruct_fwd(int dtype, const void* lengths, const void* angles, con
  * Forward reconstruction that also classifies each chain for the position-based backward:
  * chain_regular[b] = 1 when every bond length is positive, every bond angle has sin >= 0.5
  * (float32; 1e-2 for float64), every coordinate lies within 256 (float32; 8192 for float64)
- * shortest bonds of the origin, and (float32) the shortest bond is at least 2^-20; 0 otherwise
+ * shortest bonds of the origin and within 2^29 (float32; 2^250 for float64) of it, and (float32)
+ * the shortest bond is at least 2^-20; 0 otherwise
  * and always 0 for float16/bfloat16.  Same inputs and
  * output as cufk_reconstruct_fwd; chain_regular is a (B,) byte array.  No reference counterpart:
  * the reference's forward (block.cu:319-329) saves only the inputs.

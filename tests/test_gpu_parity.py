@@ -748,3 +748,20 @@ def test_angles_beyond_the_polynomial_range(cufk, device, dtype):
         ee = (np.abs(e_.double().cpu().numpy() - r) / scale).max()
         print(f"{dtype} wide-range d/d{name}: saved rel {es:.2e}, exact rel {ee:.2e}")
         assert es <= tol and ee <= tol
+
+
+def test_huge_chain_is_not_regular_in_fp32(cufk, device):
+    """Coordinates beyond 2^29 keep float32 chains off the position-based adjoint (whose squared
+    bond normals would overflow float); the exact path still matches the oracle."""
+    lib = _abi()
+    d = _inputs(3, 60, seed=29, anchors=False, dtype=torch.float32)
+    d["lengths"][1] = _round(d["lengths"][1] * 7.0e10, torch.float32)  # bonds of about 1e10: |b1 x b2|^2 > FLT_MAX
+    L, A, D = (_dev(d[k], torch.float32, device) for k in ("lengths", "angles", "dihedrals"))
+    _, reg = _flagged_forward(lib, L, A, D, _anchors3(d, torch.float32, device))
+    assert reg.cpu().tolist() == [1, 0, 1]
+    _, grads = _run(cufk, d, torch.float32, device)
+    ref = o.reconstruct_backward(d["lengths"], d["angles"], d["dihedrals"], d["grad"])
+    for got, want in zip(grads, ref):
+        assert torch.isfinite(got).all()
+        err = np.abs(got.double().cpu().numpy() - want).max(axis=1) / np.abs(want).max(axis=1)
+        assert err.max() <= 5e-5, err
