@@ -105,10 +105,10 @@ __device__ __forceinline__ void store_anchor_sums(double* __restrict__ out, V3<R
 // Guard only items < count run; without it every item runs, and the caller has padded the
 // lane's tail (pad_lane_tail) or ignores the lane.  ok and lmin accumulate the regularity
 // tests (Fast::kSinMin).  With Table, float angles take sin/cos from the LDS table.  Checked
-// selects the sin/cos form that handles angles beyond kWideReduceMax.  With Sched every item
-// is a scheduling region of its own, which keeps the independent sin/cos of later items from
-// being hoisted (and held in registers) where the compiler would otherwise do so.
-template <typename T, int K, bool Checked, bool Guard, bool Table, bool Sched, typename Fast = FastPath<T>>
+// selects the sin/cos form that handles angles beyond kWideReduceMax.  Every item is a
+// scheduling region of its own, which keeps the independent sin/cos of later items from being
+// hoisted (and held in registers) where the compiler would otherwise do so.
+template <typename T, int K, bool Checked, bool Guard, bool Table, typename Fast = FastPath<T>>
 __device__ __forceinline__ void lane_scan(const compute_t<T>* Ls, const compute_t<T>* As, const compute_t<T>* Ds,
                                           int count, const SinCosEntry* table, Rigid<double>& q,
                                           compute_t<T> (&y)[K][3], bool& ok, compute_t<T>& lmin) {
@@ -135,7 +135,7 @@ __device__ __forceinline__ void lane_scan(const compute_t<T>* Ls, const compute_
     y[i][0] = static_cast<R>(q.v[0]);
     y[i][1] = static_cast<R>(q.v[1]);
     y[i][2] = static_cast<R>(q.v[2]);
-    if constexpr (Sched) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -158,16 +158,16 @@ __device__ __forceinline__ void pad_lane_tail(R* Ls, R* As, R* Ds, int count) {
 // lanes past it scan garbage that reaches no stored point and reset their flags), the
 // library-sin/cos instance guarded and one region per item (unguarded or unscheduled it needs
 // more registers than the hot one).
-template <typename T, int K, bool Table, bool Sched, typename Fast = FastPath<T>>
+template <typename T, int K, bool Table, typename Fast = FastPath<T>>
 __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const compute_t<T>* As,
                                                 const compute_t<T>* Ds, int count, bool wave_has_steps, bool wide,
                                                 const SinCosEntry* table, Rigid<double>& q, compute_t<T> (&y)[K][3],
                                                 bool& ok, compute_t<T>& lmin) {
   if (wave_has_steps) {  // uniform per wave
     if (wide)
-      lane_scan<T, K, true, true, Table, true, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
+      lane_scan<T, K, true, true, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
     else
-      lane_scan<T, K, false, false, Table, Sched, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
+      lane_scan<T, K, false, false, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
   }
   if (count <= 0) {
     ok = true;
@@ -198,7 +198,7 @@ __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const co
 // Shadow (float16/bfloat16 whole chains): the positions are also stored unrounded, in float,
 // to shadow (the chain's (points, 3) row), and *regular receives the float32 chains' test
 // (FastPath<float>) on them, for the position-based backward over that copy.
-template <typename T, typename Lay, bool Segmented, int LossKind = kLossNone, bool Shadow = false, bool Lat = false>
+template <typename T, typename Lay, bool Segmented, int LossKind = kLossNone, bool Shadow = false>
 __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T* __restrict__ Ar,
                                               const T* __restrict__ Dr, const T* __restrict__ p0,
                                               const T* __restrict__ first_direction,
@@ -237,7 +237,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     const T* const src[3] = {Lr + 2, Ar + 1, Dr};
     wide = load_step_rows<Lay, 3, 0b110u>(dst, src, steps, tid);
   }
-  if constexpr (sizeof(R) == 4 && !Lat) sin_cos_table_init(sc_table, tid, Lay::kLanes);
+  if constexpr (sizeof(R) == 4) sin_cos_table_init(sc_table, tid, Lay::kLanes);
   if constexpr (!Segmented) pad_lane_tail<K>(stage + b0, stage + Lay::kStepRow + b0, stage + 2 * Lay::kStepRow + b0, count);
   // Loss: the target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
@@ -257,17 +257,14 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     const R* const Ls = stage + b0;
     const R* const As = stage + Lay::kStepRow + b0;
     const R* const Ds = stage + 2 * Lay::kStepRow + b0;
-    // Lat (small batches, a wave or two per SIMD, where latency rather than issue bounds the
-    // scan): sin/cos from the polynomial, not the LDS table, and no scheduling barriers, so the
-    // compiler may overlap the items' loads and sin/cos.
-    constexpr bool kTable = sizeof(R) == 4 && !Lat;
+    constexpr bool kTable = sizeof(R) == 4;
     if constexpr (Segmented) {
       if (wide)
-        lane_scan<T, K, true, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
+        lane_scan<T, K, true, true, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
       else
-        lane_scan<T, K, false, true, kTable, true>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
+        lane_scan<T, K, false, true, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
-      lane_scan_chain<T, K, kTable, !Lat, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
+      lane_scan_chain<T, K, kTable, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
                                                 lmin);
     }
   }
@@ -388,13 +385,13 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   if constexpr (Shadow) store_point_row<Lay>(shadow, stage, points, tid);
 }
 
-template <typename T, int W, int K, int Pad = 4, bool Lat = false>
+template <typename T, int W, int K, int Pad = 4>
 __global__ __launch_bounds__(64 * W) void reconstruct_forward_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ dihedrals,
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     T* __restrict__ xyz, uint8_t* __restrict__ regular, int points) {
   const int64_t row = blockIdx.x;
-  forward_chain<T, Layout<W, K, Pad>, false, kLossNone, false, Lat>(lengths + row * (points - 1), angles + row * (points - 2),
+  forward_chain<T, Layout<W, K, Pad>, false, kLossNone, false>(lengths + row * (points - 1), angles + row * (points - 2),
                                              dihedrals + row * (points - 3), p0, first_direction, initial_normal,
                                              xyz + row * points * 3, regular != nullptr ? regular + row : nullptr,
                                              points, true, nullptr);
@@ -837,7 +834,7 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
-  lane_scan_chain<T, K, false, true, Fast>(pstage + b0, pstage + Lay::kStepRow + b0, pstage + 2 * Lay::kStepRow + b0,
+  lane_scan_chain<T, K, false, Fast>(pstage + b0, pstage + Lay::kStepRow + b0, pstage + 2 * Lay::kStepRow + b0,
                                            count, wave * 64 * K < steps, wide, nullptr, q, y, ok, lmin);
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
 
