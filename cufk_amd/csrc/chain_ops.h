@@ -102,13 +102,16 @@ __device__ __forceinline__ void sin_cos_wide(float xf, double& s, double& c) {
 //   t = x * 64/pi + 1.5 * 2^52 rounds k = rint(64 x / pi) into the low mantissa bits of t,
 //   r = x - k pi/64 (one-part reduction: |r| <= pi/128, absolute error <= |k| 2^-58, i.e.
 //       4.4e-16 for |x| <= 2 pi and 4.7e-12 at kWideReduceMax),
-//   sin r = r + r u (s1 + s2 u),  cos r = 1 + w,  w = u (c2 u - 1/2),  u = r^2
-//   (near-minimax fits on [0, (pi/128)^2], the cos one with its u term held at -1/2, an
-//   inline constant: |error| < 1.4e-16 and < 3.3e-14),
+//   sin r = r + s1 r u,  cos r = 1 + w,  w = u (c2 u - 1/2),  u = r^2
+//   (s1 the minimax cubic term on |r| <= pi/128, solved for equal-ripple absolute error:
+//   |error| < 9.8e-12; c2 a near-minimax fit with the u term held at -1/2, an inline
+//   constant: |error| < 3.3e-14),
 //   sin x = T_s[k] + T_s[k] w + T_c[k] sin r,  cos x = T_c[k] + T_c[k] w - T_s[k] sin r
 // with (T_s, T_c)[j] = (sin, cos)(j pi/64) held in LDS (sin_cos_table_init) and indexed by the
-// low 7 bits of t.  No quadrant selects or conversions to integer: 17 VALU issues.  Same
-// Checked convention as sin_cos_wide.
+// low 7 bits of t.  No quadrant selects or conversions to integer: 15 VALU issues.  The
+// cubic sine keeps sin^2 + cos^2 within 1e-12 of 1 (what would bias a long float chain) and
+// each angle within 1e-11; float outputs resolve 6e-8.  Same Checked convention as
+// sin_cos_wide.
 struct __align__(16) SinCosEntry {
   double s, c;
 };
@@ -253,8 +256,7 @@ __device__ __forceinline__ void sin_cos_tab(float xf, const SinCosEntry* table, 
   const double k = t - kRound;
   const double r = fma(-k, 0.04908738521234052, x);
   const double u = r * r;
-  const double ps = lin_sk(u, 0.008333213811818094, -0.1666666666576668);
-  const double sr = fma(r * u, ps, r);
+  const double sr = fma(r * u, -0.16666230391787032, r);
   const double pc = fma_sk_minus_half(u, 0.04166591860459361);
   const double w = u * pc;
   const SinCosEntry e = table[static_cast<uint32_t>(__builtin_bit_cast(uint64_t, t)) & (kSinCosTable - 1)];
