@@ -199,8 +199,8 @@ __device__ __forceinline__ bool stage_flat(compute_t<T>* dst, const T* __restric
   return wide;
 }
 
-// dst[f] = src[fslot<Gap>(f)] for f in [0, total).
-template <int Lanes, int Gap, typename T>
+// dst[f] = src[fslot<Gap>(f)] for f in [0, total); Stream as for global_store.
+template <int Lanes, int Gap, bool Stream = false, typename T>
 __device__ __forceinline__ void store_flat(T* __restrict__ dst, const compute_t<T>* src, int total, int tid) {
   constexpr int E = 16 / sizeof(T);
   static_assert(E <= Gap, "a window crosses at most one segment end");
@@ -211,14 +211,14 @@ __device__ __forceinline__ void store_flat(T* __restrict__ dst, const compute_t<
     T v[E];
 #pragma unroll
     for (int k = 0; k < E; ++k) v[k] = narrow<T>(src[run.slot(k)]);
-    uint4 w;
+    u32x4 w;
     __builtin_memcpy(&w, v, 16);
-    *reinterpret_cast<uint4*>(dst + f0) = w;
+    global_store<Stream>(reinterpret_cast<u32x4*>(dst + f0), w);
   }
-  if (tid < sp.head) dst[tid] = narrow<T>(src[fslot<Gap>(tid)]);
+  if (tid < sp.head) global_store<Stream>(dst + tid, narrow<T>(src[fslot<Gap>(tid)]));
   if (tid < sp.tail) {
     const int f = total - sp.tail + tid;
-    dst[f] = narrow<T>(src[fslot<Gap>(f)]);
+    global_store<Stream>(dst + f, narrow<T>(src[fslot<Gap>(f)]));
   }
 }
 
@@ -780,9 +780,9 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
     }
   }
   __syncthreads();
-  store_flat<P::kLanes, P::kStepGap>(grad_lengths + b0 * (points - 1), ol, nc * (points - 1), tid);
-  store_flat<P::kLanes, P::kStepGap>(grad_angles + b0 * (points - 2), oa, nc * (points - 2), tid);
-  store_flat<P::kLanes, P::kStepGap>(grad_dihedrals + b0 * (points - 3), od, nc * (points - 3), tid);
+  store_flat<P::kLanes, P::kStepGap, true>(grad_lengths + b0 * (points - 1), ol, nc * (points - 1), tid);
+  store_flat<P::kLanes, P::kStepGap, true>(grad_angles + b0 * (points - 2), oa, nc * (points - 2), tid);
+  store_flat<P::kLanes, P::kStepGap, true>(grad_dihedrals + b0 * (points - 3), od, nc * (points - 3), tid);
 }
 
 }  // namespace cufk_amd

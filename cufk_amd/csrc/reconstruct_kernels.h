@@ -392,7 +392,8 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     *regular = reg ? 1 : 0;
   }
   if constexpr (Loss) lossacc.template finish<T, W>(loss, record, lane, wave, tid);
-  store_point_row<Lay>(out, stage, points, tid, !Segmented || head);
+  // A half-type chain's backward reads the float copy, not the rounded output.
+  store_point_row<Lay, Shadow>(out, stage, points, tid, !Segmented || head);
   if constexpr (Shadow) store_point_row<Lay>(shadow, stage, points, tid);
 }
 

@@ -282,7 +282,7 @@ __global__ __launch_bounds__(64 * W) void torsion_backward_kernel(const T* __res
       go[2 * i + 1] = -rs * scale;
     }
   }
-  store_run<2 * K>(graw + 2 * s0, 2 * count, go);
+  store_run<2 * K>(graw + 2 * s0, 2 * count, go);  // per-lane runs: nontemporal measured slower
 }
 
 }  // namespace cufk_amd
