@@ -87,9 +87,9 @@ ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 # each counter scaled by what it reads for a plain copy of known size; the per-kernel figures are
 # in profiles/hbm_traffic_c2_c3_c4.md.  A config without an entry reports traffic as null.
 MEASURED_TRAFFIC = {
-    "c2": 203296092 + 303465350,  # forward (read 102434140, write 100861952) + backward (202636371 + 100828979)
-    "c3": 126570527 + 254119503,  # torsion forward (50548153 + 76022374) + backward (203780687 + 50338816)
-    "c4_bf16": 409686435 + 408598374,  # forward with the float copy (106083543 + 303602893) + backward (306951629 + 101646746)
+    "c2": 203257551 + 307661823,  # forward (read 102397237, write 100860314) + backward (202647346 + 105014477)
+    "c3": 126591291 + 254078872,  # torsion forward (50569224 + 76022067) + backward (203743538 + 50335334)
+    "c4_bf16": 415663340 + 411567446,  # forward with the float copy (105390111 + 310273229) + backward (306882902 + 104684544)
 }
 
 
