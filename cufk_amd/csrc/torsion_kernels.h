@@ -112,6 +112,14 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
 
   load_pair_rows<Lay>(stage, stage + Lay::kStepRow, raw, steps, tid);
   const int s0 = tid * K;
+  const int b0 = Lay::lane_step_base(tid);
+  // Items past the chain's end take the pair (0, 1), a zero torsion, so that every lane runs
+  // its K items without a guard (no exec-mask branches or register copies per item); their
+  // positions are never stored.
+  for (int i = steps - s0 > 0 ? steps - s0 : 0; i < K; ++i) {
+    stage[b0 + i] = R(0);
+    stage[Lay::kStepRow + b0 + i] = R(1);
+  }
   const T* tgt = Loss ? target + row * points * 3 : nullptr;
   // The target of the lane's own points, loaded now so that the scan hides the latency.
   R tr[Loss ? 3 * K : 1];
@@ -125,19 +133,17 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
   // the compute type, torsion.cu:226-227, which biases |M| per phase along the chain).
   Rigid<double> q = rigid_identity<double>();
   R y[K][3];
-  const int b0 = Lay::lane_step_base(tid);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    if (s0 + i < steps) {
-      const int lp = (i + 2) % 3;  // torsion.cu:67-69
-      const int ap = (i + 1) % 3;  // torsion.cu:71-73
-      double S, C;
-      pair_unit(stage[b0 + i], stage[Lay::kStepRow + b0 + i], S, C);
-      step_forward(q.m, q.v, static_cast<double>(cst.length[lp]), cst.sin[ap], cst.cos[ap], S, C);
-    }
+    const int lp = (i + 2) % 3;  // torsion.cu:67-69
+    const int ap = (i + 1) % 3;  // torsion.cu:71-73
+    double S, C;
+    pair_unit(stage[b0 + i], stage[Lay::kStepRow + b0 + i], S, C);
+    step_forward(q.m, q.v, static_cast<double>(cst.length[lp]), cst.sin[ap], cst.cos[ap], S, C);
     y[i][0] = static_cast<R>(q.v[0]);
     y[i][1] = static_cast<R>(q.v[1]);
     y[i][2] = static_cast<R>(q.v[2]);
+    __builtin_amdgcn_sched_barrier(0);  // one item per scheduling region: no hoisting across items
   }
 
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
