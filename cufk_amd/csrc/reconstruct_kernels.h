@@ -269,6 +269,8 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     if constexpr (Segmented) {
       if (wide)
         lane_scan<T, K, true, true, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
+      else if ((wave + 1) * 64 * K <= steps)  // every lane of the wave has K steps: no guard
+        lane_scan<T, K, false, false, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
       else
         lane_scan<T, K, false, true, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
