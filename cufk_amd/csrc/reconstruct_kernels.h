@@ -298,11 +298,30 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
     }
   }
 
+  // Segments: the lane with the last step parks its double transform in LDS for the segment's
+  // total, so that no lane holds it in registers across the carry (107 -> 88 VGPRs).
+  __shared__ double last_q[Segmented ? 12 : 1];
+  const bool last_lane = count > 0 && count + s0 == steps;
+  if constexpr (Segmented) {
+    if (last_lane) {
+#pragma unroll
+      for (int i = 0; i < 9; ++i) last_q[i] = q.m[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) last_q[9 + i] = q.v[i];
+    }
+  }
   // lane_carry's barrier also publishes base[] and retires every read of the staged step
   // rows, which the point row below overwrites.
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
   if constexpr (Segmented) {
-    if (count > 0 && count + s0 == steps) store_total(total, excl, q);  // the lane with the last step
+    if (last_lane) {
+      Rigid<double> qt;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) qt.m[i] = last_q[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) qt.v[i] = last_q[9 + i];
+      store_total(total, excl, qt);
+    }
   }
   R F[9];
 #pragma unroll
