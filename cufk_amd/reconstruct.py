@@ -27,10 +27,21 @@ def _batched_inputs(
     return lengths, angles, dihedrals, single
 
 
+_DEFAULT_ANCHORS: dict[tuple[torch.device, torch.dtype, tuple[float, float, float]], torch.Tensor] = {}
+
+
 def _anchor(x: torch.Tensor | None, vals: tuple[float, float, float], ref: torch.Tensor) -> torch.Tensor:
-    """reconstruct.py:19-26: default anchor on ``ref``'s device and dtype."""
+    """reconstruct.py:19-26: default anchor on ``ref``'s device and dtype.
+
+    The reference builds it with a host-to-device copy on every call.  Here it is built once per
+    device, dtype and value and reused: the kernels only read it and it never requires grad, so
+    the values and gradients are the same, and a call with default anchors saves three small
+    copies (about 45 us of host time at C1's size)."""
     if x is None:
-        x = torch.tensor(vals, device=ref.device, dtype=ref.dtype)
+        key = (ref.device, ref.dtype, vals)
+        x = _DEFAULT_ANCHORS.get(key)
+        if x is None:
+            x = _DEFAULT_ANCHORS.setdefault(key, torch.tensor(vals, device=ref.device, dtype=ref.dtype))
     return x
 
 

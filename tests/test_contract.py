@@ -167,6 +167,12 @@ def test_batching_and_default_anchors():
     assert a.dtype == torch.float64 and a.tolist() == [1.0, 0.0, 0.0]
     given = torch.ones(3)
     assert rmod._anchor(given, (0.0, 0.0, 0.0), ref) is given
+    # Defaults are built once per device, dtype and value, and keep their values.
+    assert rmod._anchor(None, (1.0, 0.0, 0.0), ref) is a
+    b = rmod._anchor(None, (0.0, 0.0, 1.0), ref)
+    assert b is not a and b.tolist() == [0.0, 0.0, 1.0] and not b.requires_grad
+    c = rmod._anchor(None, (1.0, 0.0, 0.0), ref.float())
+    assert c.dtype == torch.float32 and c.tolist() == [1.0, 0.0, 0.0]
 
 
 def test_max_steps():
