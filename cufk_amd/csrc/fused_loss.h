@@ -69,28 +69,57 @@ __device__ __forceinline__ auto make_residual(R w, const double* __restrict__ re
 }
 
 // Per-thread accumulation of a chain's loss from its stored positions xs (rounded to the
-// storage type, in the compute type R) and the target t.  The superposed sums are taken about
-// the shift points cx (the chain's stored x2) and ct (the target's point 2), per thread in R
-// over its at most 12 points (float32: about 1e-7 relative of a few products, which leaves the
-// superposed msd good to about 1e-6 relative at N = 2049), then in double across threads.
+// storage type, in the compute type R) and the target t.
+//
+// The superposed sums are the chain's moments about the shift points cx (its stored x2) and ct
+// (the target's point 2), which the solve centres (S = sum x' t'^T - N xbar tbar^T) and cancels
+// (msd = (sum |x'|^2 + sum |t'|^2 - 2 lambda) / N, about 250x at N = 2049 with 0.3 nm of noise),
+// so their rounding is amplified: summed in float about cx and ct, the products' 1e-7 relative
+// rounding at the chain's extent turned the solved rotation by a few 1e-7, which leaves the
+// residual with a net torque that the adjoint's moment sums add up along the chain (measured at
+// the C2 shape: 1e-4 relative gradient error on 98 of 4096 chains, the RMSD 9e-6 relative off).
+// So each thread sums about its own first point and that point's target (xl, tl), which its at
+// most 15 points stay within a few nanometres of: the nine products and two squares in R (their
+// rounding is now that of a few nm^2), the six first moments in double (they are later
+// multiplied by the thread's distance from the chain's centroid).  finish() moves the sums to
+// cx and ct in double (superpose_move; e = xl - cx and f = tl - ct are exact there) before the
+// cross-thread reduction.  Against all 17 sums in double per point this takes 12 double
+// operations per point instead of 33 and no more VGPRs than float sums (measured at the C2
+// shape: the RMSD step 2-3 % slower than with float sums, against 9 % all in double).
 template <int LossKind, typename R> struct LossAccumulator {
+  static constexpr bool kSuperposed = LossKind == kLossSuperposed;
   double acc = 0.0;
-  R sp[LossKind == kLossSuperposed ? kSuperposeSums : 1] = {};
-  V3<R> cx = {R(0), R(0), R(0)}, ct = {R(0), R(0), R(0)};
+  double s1[kSuperposed ? 6 : 1] = {};   // sum a, sum b (about xl, tl)
+  R s2[kSuperposed ? 11 : 1] = {};       // sum a b^T (row-major), sum |a|^2, sum |b|^2
+  int m = 0;                             // points summed by this thread
+  V3<R> cx = {R(0), R(0), R(0)}, ct = {R(0), R(0), R(0)};  // the chain's shift points
+  V3<R> xl = {R(0), R(0), R(0)}, tl = {R(0), R(0), R(0)};  // this thread's
+
+  // Superposed: the chain's shift points, which are also the thread's until local_shift()
+  // gives it its own (its first point and that point's target).
+  __device__ __forceinline__ void chain_shift(V3<R> x, V3<R> t) {
+    cx = xl = x;
+    ct = tl = t;
+  }
+  __device__ __forceinline__ void local_shift(V3<R> x, V3<R> t) {
+    xl = x;
+    tl = t;
+  }
 
   __device__ __forceinline__ void add(V3<R> xs, V3<R> t) {
-    if constexpr (LossKind == kLossSuperposed) {
-      const V3<R> xd = xs - cx, td = t - ct;
-      const R a[3] = {xd.x, xd.y, xd.z}, b[3] = {td.x, td.y, td.z};
+    if constexpr (kSuperposed) {
+      const V3<R> av = xs - xl, bv = t - tl;
+      const R a[3] = {av.x, av.y, av.z}, b[3] = {bv.x, bv.y, bv.z};
 #pragma unroll
       for (int i = 0; i < 3; ++i) {
-        sp[i] += a[i];
-        sp[3 + i] += b[i];
+        s1[i] += static_cast<double>(a[i]);
+        s1[3 + i] += static_cast<double>(b[i]);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) sp[6 + 3 * i + j] += a[i] * b[j];
+        for (int j = 0; j < 3; ++j) s2[3 * i + j] = fma(a[i], b[j], s2[3 * i + j]);
       }
-      sp[15] += dot(xd, xd);
-      sp[16] += dot(td, td);
+      s2[9] = fma(a[2], a[2], fma(a[1], a[1], fma(a[0], a[0], s2[9])));
+      s2[10] = fma(b[2], b[2], fma(b[1], b[1], fma(b[0], b[0], s2[10])));
+      ++m;
     } else {
       const V3<R> d = xs - t;
       acc += static_cast<double>(dot(d, d));
@@ -104,10 +133,22 @@ template <int LossKind, typename R> struct LossAccumulator {
   __device__ __forceinline__ void finish(T* __restrict__ loss, double* __restrict__ record, int lane, int wave,
                                          int tid) {
     if constexpr (LossKind == kLossSuperposed) {
+      // This thread's sums moved to the chain's shift points, in double.
+      const double e[3] = {static_cast<double>(xl.x) - static_cast<double>(cx.x),
+                           static_cast<double>(xl.y) - static_cast<double>(cx.y),
+                           static_cast<double>(xl.z) - static_cast<double>(cx.z)};
+      const double f[3] = {static_cast<double>(tl.x) - static_cast<double>(ct.x),
+                           static_cast<double>(tl.y) - static_cast<double>(ct.y),
+                           static_cast<double>(tl.z) - static_cast<double>(ct.z)};
+      double s2d[11];
+#pragma unroll
+      for (int k = 0; k < 11; ++k) s2d[k] = static_cast<double>(s2[k]);
+      double sp[kSuperposeSums];
+      superpose_move(s1, s2d, static_cast<double>(m), e, f, sp);
       __shared__ double part[W][kSuperposeSums];
 #pragma unroll
       for (int k = 0; k < kSuperposeSums; ++k) {
-        const double v = wave_sum(static_cast<double>(sp[k]));
+        const double v = wave_sum(sp[k]);
         if (lane == 0) part[wave][k] = v;
       }
       __syncthreads();

@@ -339,11 +339,11 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
 
   R xmax = R(0);
   // The fused loss's share of this thread; superposed sums about the stored x2 and the
-  // target's point 2.
+  // target's point 2 for the chain, the thread's first point and its target for the thread.
   LossAccumulator<LossKind, R> lossacc;
   if constexpr (Superposed) {
-    lossacc.cx = {widen(narrow<T>(p2.x)), widen(narrow<T>(p2.y)), widen(narrow<T>(p2.z))};
-    lossacc.ct = {widen(target[6]), widen(target[7]), widen(target[8])};
+    lossacc.chain_shift(V3<R>{widen(narrow<T>(p2.x)), widen(narrow<T>(p2.y)), widen(narrow<T>(p2.z))},
+                        V3<R>{widen(target[6]), widen(target[7]), widen(target[8])});
   }
   {
     const int o0 = Lay::lane_point_base(tid);
@@ -356,6 +356,9 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
                          fma(gm[8], y[i][2], fma(gm[7], y[i][1], fma(gm[6], y[i][0], gv.z)))};
         if constexpr (Loss) {
           const V3<R> xs = {widen(narrow<T>(x.x)), widen(narrow<T>(x.y)), widen(narrow<T>(x.z))};
+          if constexpr (Superposed) {
+            if (i == 0) lossacc.local_shift(xs, V3<R>{tr[0], tr[1], tr[2]});
+          }
           lossacc.add(xs, V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]});
         }
         stage[o0 + 3 * i] = x.x;

@@ -45,6 +45,29 @@ CUFK_HD inline void superpose_add(double (&s)[kSuperposeSums], const double (&x)
   s[16] += t[0] * t[0] + t[1] * t[1] + t[2] * t[2];
 }
 
+// A part of the chain summed about its own shift points (xl, tl), moved to the chain's (cx, ct).
+// s1 = [sum a, sum b] and s2 = [sum a b^T (row-major), sum |a|^2, sum |b|^2] over its m points,
+// a = x - xl, b = t - tl; e = xl - cx, f = tl - ct.  With x - cx = a + e and t - ct = b + f:
+//   sum (a + e) = sum a + m e,
+//   sum (a + e)(b + f)^T = sum a b^T + (sum a) f^T + e (sum b + m f)^T,
+//   sum |a + e|^2 = sum |a|^2 + 2 e . sum a + m |e|^2   (and the same for b, f).
+CUFK_HD inline void superpose_move(const double (&s1)[6], const double (&s2)[11], double m, const double (&e)[3],
+                                   const double (&f)[3], double (&out)[kSuperposeSums]) {
+  double ea = 0.0, fb = 0.0, ee = 0.0, ff = 0.0;
+  for (int i = 0; i < 3; ++i) {
+    out[i] = s1[i] + m * e[i];
+    out[3 + i] = s1[3 + i] + m * f[i];
+    ea += e[i] * s1[i];
+    fb += f[i] * s1[3 + i];
+    ee += e[i] * e[i];
+    ff += f[i] * f[i];
+  }
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) out[6 + 3 * i + j] = s2[3 * i + j] + s1[i] * f[j] + e[i] * out[3 + j];
+  out[15] = s2[9] + 2.0 * ea + m * ee;
+  out[16] = s2[10] + 2.0 * fb + m * ff;
+}
+
 // A chain's record, 24 doubles.  The fused forward writes the sums (kSuperposeSums) and the
 // shift points cx (at 17) and ct (at 20); superpose_solve_record then replaces them with what
 // the backward needs:

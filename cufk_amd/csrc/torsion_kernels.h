@@ -165,16 +165,21 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
 
   LossAccumulator<LossKind, R> lossacc;
   auto stored = [](V3<R> x) { return V3<R>{widen(narrow<T>(x.x)), widen(narrow<T>(x.y)), widen(narrow<T>(x.z))}; };
-  if constexpr (LossKind == kLossSuperposed) {
-    lossacc.cx = stored(p2);
-    lossacc.ct = {widen(tgt[6]), widen(tgt[7]), widen(tgt[8])};
-  }
+  // Superposed sums about the stored x2 and the target's point 2 for the chain, the thread's
+  // first point and its target for the thread.
+  if constexpr (LossKind == kLossSuperposed) lossacc.chain_shift(stored(p2), V3<R>{widen(tgt[6]), widen(tgt[7]), widen(tgt[8])});
   const int o0 = Lay::lane_point_base(tid);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (s0 + i < steps) {
       const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
-      if constexpr (Loss) lossacc.add(stored(x), V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]});
+      if constexpr (Loss) {
+        const V3<R> xs = stored(x);
+        if constexpr (LossKind == kLossSuperposed) {
+          if (i == 0) lossacc.local_shift(xs, V3<R>{tr[0], tr[1], tr[2]});
+        }
+        lossacc.add(xs, V3<R>{tr[3 * i], tr[3 * i + 1], tr[3 * i + 2]});
+      }
       stage[o0 + 3 * i] = x.x;
       stage[o0 + 3 * i + 1] = x.y;
       stage[o0 + 3 * i + 2] = x.z;

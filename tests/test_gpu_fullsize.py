@@ -1,4 +1,4 @@
-"""Every chain of the BASELINE configs at full size, and the committed fixtures, on the GPU.
+"""Every chain of the benchmark configurations at full size, and the committed fixtures, on the GPU.
 
 The float64 checker for full batches is oracle/cpu_torch.py (the reference algorithm in
 PyTorch float64, pinned to oracle/nerf64.py in tests/test_oracle.py) run on the device: a serial
@@ -10,7 +10,10 @@ NeRF forward and the explicit world-frame reverse adjoint.  Bars:
   device: bond lengths, bond angles and dihedrals recovered from the stored coordinates agree
   with the inputs within what float32 rounding at the chain's extent allows (derived in
   `_check_roundtrip`);
-* float16/bfloat16 (C4): reported, held to sanity bounds.
+* float16/bfloat16 (C4): reported, held to sanity bounds;
+* the fused losses (coordinate loss, superposed RMSD and mean squared deviation) at the C2 and
+  C3 shapes: loss per chain within 1e-5 relative, gradients per chain against the float64
+  adjoint over the stored positions (derived in `_check_fused`).
 """
 
 from __future__ import annotations
@@ -38,7 +41,7 @@ def cufk(device):
 
 
 def _synthetic(B, N, seed, device):
-    """BASELINE draws (float64 on the CPU, then moved): lengths ~N(0.145, 0.01) clipped to
+    """The benchmark draws (float64 on the CPU, then moved): lengths ~N(0.145, 0.01) clipped to
     [0.12, 0.17], angles ~N(2.05, 0.08), dihedrals ~U(-pi, pi), grad ~N(0, 1), random anchors."""
     gen = torch.Generator().manual_seed(seed)
     L = (torch.randn(B, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
@@ -194,6 +197,122 @@ def test_config4_every_chain_reported(cufk, device, dtype):
         err = _per_chain_rel(got, w)
         print(f"C4 {dtype} d/d{name}: worst per-chain rel err {err.max():.2e}")
         assert bool(torch.isfinite(got).all()) and bool((err <= 3e-2).all())
+
+
+# ----------------------------------------------------------------- fused losses, every chain
+
+
+def _target(xyz64, seed, rotate):
+    """A target per chain: the float64 chain, rigidly moved when ``rotate`` (one proper rotation
+    and a 4 nm shift for the batch, so the superposition has work to do), plus N(0, 0.3 nm)
+    noise per coordinate; rounded to float32, whose float64 value is returned."""
+    gen = torch.Generator().manual_seed(seed)
+    dev = xyz64.device
+    noise = (torch.randn(*xyz64.shape, generator=gen, dtype=torch.float64) * 0.3).to(dev)
+    t = xyz64 + noise
+    if rotate:
+        q, _ = torch.linalg.qr(torch.randn(3, 3, generator=gen, dtype=torch.float64))
+        q = q * torch.sign(torch.linalg.det(q))
+        shift = torch.randn(3, generator=gen, dtype=torch.float64) * 4.0
+        t = xyz64 @ q.T.contiguous().to(dev) + shift.to(dev) + noise
+    return t.float().double()
+
+
+def _loss_refs(kind, ref, xs, t64):
+    """float64 loss of the float64 chain, and grad_xyz over the stored positions ``xs`` (the
+    fused backward differentiates the loss of the positions it stored)."""
+    if kind == "loss":
+        return ((ref - t64) ** 2).sum((1, 2)), 2.0 * (xs - t64)
+    sq = kind == "msd"
+    tn = t64.cpu().numpy()
+    loss = o.superposed_loss(ref.cpu().numpy(), tn, sq)
+    gx = o.superposed_grad_xyz(xs.cpu().numpy(), tn, None, sq)
+    return torch.as_tensor(loss).to(ref.device), torch.as_tensor(gx).to(ref.device)
+
+
+def _unfused_loss(kind, x, t64):
+    """The same loss in torch over the unfused output ``x``; for the superposed kinds the
+    rotation is solved on the host (oracle/nerf64.py superpose, SVD) from x's values and held
+    fixed, its own dependence dropping out at the optimum."""
+    t = t64.to(x.dtype)
+    if kind == "loss":
+        return ((x - t) ** 2).sum((1, 2))
+    R, _, _, _ = o.superpose(x.detach().double().cpu().numpy(), t64.cpu().numpy())
+    Rt = torch.as_tensor(R).to(device=x.device, dtype=x.dtype).transpose(1, 2).contiguous()
+    msd = ((x - x.mean(1, keepdim=True)) @ Rt - (t - t.mean(1, keepdim=True))).pow(2).sum(-1).mean(-1)
+    return msd if kind == "msd" else msd.sqrt()
+
+
+def _check_fused(kind, label, loss, unfused, want_loss, grads, ugrads, adj):
+    """Loss per chain within 1e-5 relative of the float64 chain's and of the unfused composition;
+    gradients per chain within 5e-5 relative of the float64 adjoint over the stored positions.
+    A superposed loss is invariant under rigid motions, so its grad_xyz has zero net force and
+    torque and the adjoint's float32 suffix sums end in the remainder of a cancelling sum; there
+    the bar is the larger of 5e-5 and 1.5x the unfused composition's own error on that chain
+    (reconstruct's backward over the same grad_xyz carries the same amplification)."""
+    lerr = (loss.detach().double() - want_loss).abs() / want_loss.abs()
+    uerr = (loss.detach() - unfused.detach()).abs() / unfused.detach().abs()
+    print(f"{label} fused {kind}, every chain: worst loss rel err {lerr.max():.2e} against float64, "
+          f"{uerr.max():.2e} against the unfused composition")
+    assert bool((lerr <= 1e-5).all()) and bool((uerr <= 1e-5).all())
+    for name, got, alt, w in zip(("lengths", "angles", "dihedrals", "raw pairs"), grads, ugrads, adj):
+        f = _per_chain_rel(got, w)
+        u = _per_chain_rel(alt, w)
+        bar = torch.full_like(f, 5e-5) if kind == "loss" else torch.clamp(1.5 * u, min=5e-5)
+        print(f"  d/d{name}: worst per-chain rel err fused {f.max():.2e} (chain {int(f.argmax())}), "
+              f"unfused {u.max():.2e}; chains over 5e-5: fused {int((f > 5e-5).sum())}, unfused {int((u > 5e-5).sum())}")
+        assert bool(torch.isfinite(got).all()) and bool((f <= bar).all())
+
+
+@pytest.mark.parametrize("kind", ["loss", "rmsd", "msd"])
+def test_config2_fused_losses_every_chain(cufk, device, kind):
+    """reconstruct_loss and reconstruct_rmsd (root and squared) at the C2 shape (B = 4096,
+    N = 2049, float32, random anchors), every chain, against float64 and the unfused
+    composition (reconstruct, the loss in torch, autograd)."""
+    B, N = 4096, 2049
+    L, A, D, _, p0, fd, n0 = _synthetic(B, N, 12, device)
+    f32 = [t.float() for t in (L, A, D, p0, fd, n0)]
+    ref = ct.forward(*(t.double() for t in f32))
+    t64 = _target(ref, 12, rotate=kind != "loss")
+    t32 = t64.float()
+    Lf, Af, Df = (x.clone().requires_grad_(True) for x in f32[:3])
+    if kind == "loss":
+        loss = cufk.reconstruct_loss(Lf, Af, Df, t32, *f32[3:])
+    else:
+        loss = cufk.reconstruct_rmsd(Lf, Af, Df, t32, *f32[3:], squared=kind == "msd")
+    grads = torch.autograd.grad(loss.sum(), (Lf, Af, Df))
+    Lu, Au, Du = (x.clone().requires_grad_(True) for x in f32[:3])
+    x = cufk.reconstruct(Lu, Au, Du, *f32[3:])
+    unfused = _unfused_loss(kind, x, t64)
+    ugrads = torch.autograd.grad(unfused.sum(), (Lu, Au, Du))
+    xs = x.detach().double()  # the positions the fused forward stores: the same kernel arithmetic
+    want_loss, gx = _loss_refs(kind, ref, xs, t64)
+    adj = ct.backward(xs, gx)
+    _check_fused(kind, "C2", loss, unfused, want_loss, grads, ugrads, adj)
+
+
+@pytest.mark.parametrize("kind", ["loss", "rmsd", "msd"])
+def test_config3_fused_losses_every_chain(cufk, device, kind):
+    """compile_torsion(...).loss and .rmsd (root and squared) at the C3 shape (B = 8192,
+    N = 771, float32), every chain, against float64 and the unfused composition."""
+    B, N = 8192, 771
+    gen = torch.Generator().manual_seed(13)
+    raw64 = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).float().double().to(device)
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    ref = ct.torsion_forward(raw64, c.lengths, c.sin, c.cos)
+    t64 = _target(ref, 13, rotate=kind != "loss")
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    raw = raw64.float().requires_grad_(True)
+    loss = f.loss(raw, t64.float()) if kind == "loss" else f.rmsd(raw, t64.float(), squared=kind == "msd")
+    (graw,) = torch.autograd.grad(loss.sum(), (raw,))
+    raw_u = raw64.float().requires_grad_(True)
+    x = f(raw_u)
+    unfused = _unfused_loss(kind, x, t64)
+    (ugraw,) = torch.autograd.grad(unfused.sum(), (raw_u,))
+    xs = x.detach().double()
+    want_loss, gx = _loss_refs(kind, ref, xs, t64)
+    adj = ct.torsion_backward(raw64, xs, gx, c.lengths)
+    _check_fused(kind, "C3", loss, unfused, want_loss, (graw,), (ugraw,), (adj,))
 
 
 # ----------------------------------------------------------------- committed fixtures

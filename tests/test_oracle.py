@@ -615,6 +615,88 @@ def test_superpose_header_matches_the_oracle(tmp_path):
             assert np.abs(got[9:12] - (xb[0] - R[0].T @ tb[0])).max() <= 1e-9 * max(1.0, np.abs(xb).max())
 
 
+def _superpose_move_exe(tmp_path):
+    """superpose_move of cufk_amd/csrc/superpose.h built for the host: reads m, e, f, s1, s2
+    and prints the 17 moved sums."""
+    import shutil
+    import subprocess
+
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no host C++ compiler")
+    root = Path(__file__).resolve().parent.parent
+    src = tmp_path / "mv.cpp"
+    src.write_text(
+        '#include "superpose.h"\n#include <cstdio>\nusing namespace cufk_amd;\n'
+        "int main() { double m, e[3], f[3], s1[6], s2[11];\n"
+        '  while (scanf("%lf", &m) == 1) {\n'
+        '    for (int k = 0; k < 3; ++k) if (scanf("%lf", e + k) != 1) return 1;\n'
+        '    for (int k = 0; k < 3; ++k) if (scanf("%lf", f + k) != 1) return 1;\n'
+        '    for (int k = 0; k < 6; ++k) if (scanf("%lf", s1 + k) != 1) return 1;\n'
+        '    for (int k = 0; k < 11; ++k) if (scanf("%lf", s2 + k) != 1) return 1;\n'
+        "    double out[kSuperposeSums]; superpose_move(s1, s2, m, e, f, out);\n"
+        '    for (int k = 0; k < kSuperposeSums; ++k) printf("%.17g ", out[k]); printf("\\n"); }\n  return 0; }\n'
+    )
+    exe = tmp_path / "mv"
+    subprocess.run([gxx, "-O2", "-std=c++17", f"-I{root / 'cufk_amd' / 'csrc'}", str(src), "-o", str(exe)], check=True)
+    return exe
+
+
+def _direct_sums(x, t, cx, ct):
+    """The 17 superposition sums of the points about (cx, ct), straight from their definition."""
+    a, b = x - cx, t - ct
+    return np.concatenate([a.sum(0), b.sum(0), (a[:, :, None] * b[:, None, :]).sum(0).ravel(),
+                           [np.sum(a * a), np.sum(b * b)]])
+
+
+@pytest.mark.parametrize("plant", [None, "drop_cross", "swap_ef"])
+def test_superpose_move_equals_the_direct_sums(tmp_path, plant):
+    """The fused forwards sum each thread's points about that thread's own first point and
+    target point, then move the sums to the chain's shift points with superpose_move: chains cut
+    into runs of 1 to 15 points (as threads hold them), moved and added up, equal the sums taken
+    directly about the chain's shift points (1e-12 relative).  Planted mistakes in the inputs
+    (the cross term's first moments zeroed; e and f exchanged) fail the same comparison."""
+    import subprocess
+
+    exe = _superpose_move_exe(tmp_path)
+    rng = np.random.default_rng(21)
+    chains, text = [], ""
+    for n in (4, 15, 16, 200, 2049):
+        x = np.cumsum(rng.normal(size=(n, 3)) * 0.15, axis=0) + rng.normal(size=3) * 5.0
+        t = x @ _rot(rng).T + rng.normal(size=3) * 4.0 + rng.normal(size=x.shape) * 0.3
+        cx, ct = x[2], t[2]
+        runs, i = [], 0
+        while i < n:
+            m = int(rng.integers(1, 16))
+            runs.append((i, min(n, i + m)))
+            i += m
+        chains.append((x, t, cx, ct, len(runs)))
+        for i0, i1 in runs:
+            xl, tl = x[i0], t[i0]
+            a, b = x[i0:i1] - xl, t[i0:i1] - tl
+            s1 = np.concatenate([a.sum(0), b.sum(0)])
+            if plant == "drop_cross":
+                s1 = np.zeros(6)
+            s2 = np.concatenate([(a[:, :, None] * b[:, None, :]).sum(0).ravel(), [np.sum(a * a), np.sum(b * b)]])
+            e, f = xl - cx, tl - ct
+            if plant == "swap_ef":
+                e, f = f, e
+            text += " ".join(repr(float(v)) for v in (i1 - i0, *e, *f, *s1, *s2)) + "\n"
+    out = subprocess.run([str(exe)], input=text, capture_output=True, text=True, check=True).stdout.split("\n")
+    row = 0
+    worst = 0.0
+    for x, t, cx, ct, nruns in chains:
+        moved = np.sum([[float(v) for v in out[row + r].split()] for r in range(nruns)], axis=0)
+        row += nruns
+        want = _direct_sums(x, t, cx, ct)
+        scale = np.abs(want).max()
+        worst = max(worst, np.abs(moved - want).max() / scale)
+    if plant is None:
+        assert worst <= 1e-12, worst
+    else:
+        assert worst > 1e-6, (plant, worst)
+
+
 def test_checks_catch_a_transposed_superposition(monkeypatch):
     """Planted mistake: the rotation transposed in superposed_grad_xyz's superposition.  The
     finite-difference pin above fails on it."""
