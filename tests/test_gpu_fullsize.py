@@ -11,6 +11,8 @@ NeRF forward and the explicit world-frame reverse adjoint.  Bars:
   with the inputs within what float32 rounding at the chain's extent allows (derived in
   `_check_roundtrip`);
 * float16/bfloat16 (C4): reported, held to sanity bounds;
+* the extension bench configurations, short chains (131072 x 64) and long chains (64 x 131075),
+  every chain: coordinates, round trip and gradients (derived in the tests);
 * the fused losses (coordinate loss, superposed RMSD and mean squared deviation) at the C2 and
   C3 shapes: loss per chain within 1e-5 relative, gradients per chain against the float64
   adjoint over the stored positions (derived in `_check_fused`).
@@ -197,6 +199,62 @@ def test_config4_every_chain_reported(cufk, device, dtype):
         err = _per_chain_rel(got, w)
         print(f"C4 {dtype} d/d{name}: worst per-chain rel err {err.max():.2e}")
         assert bool(torch.isfinite(got).all()) and bool((err <= 3e-2).all())
+
+
+# ----------------------------------------------------------------- extension configurations
+
+
+def _check_gradients(label, grads, want, bar):
+    for name, got, w in zip(("lengths", "angles", "dihedrals"), grads, want):
+        err = _per_chain_rel(got, w)
+        print(f"{label} every chain d/d{name}: worst per-chain rel err {err.max():.2e} (chain {int(err.argmax())})")
+        assert bool(torch.isfinite(got).all()) and bool((err <= bar).all())
+
+
+def test_short_config_every_chain(cufk, device):
+    """The short-chain bench configuration (B = 131072, N = 64, float32, random anchors: the
+    packed kernels, several chains per wave), every chain: coordinates and round trip under the
+    C2 bars, gradients within 5e-5 per chain."""
+    B, N = 131072, 64
+    L, A, D, g, p0, fd, n0 = _synthetic(B, N, 5, device)
+    f32 = [t.float() for t in (L, A, D, g, p0, fd, n0)]
+    Lf, Af, Df = (t.clone().requires_grad_(True) for t in f32[:3])
+    xyz = cufk.reconstruct(Lf, Af, Df, *f32[4:])
+    grads = torch.autograd.grad(xyz, (Lf, Af, Df), f32[3])
+    L64, A64, D64, g64 = (t.double() for t in f32[:4])
+    ref = ct.forward(L64, A64, D64, *(t.double() for t in f32[4:]))
+    _check_coordinates(xyz.detach(), ref, "short")
+    _check_roundtrip(xyz.detach(), L64, A64, D64, "short")
+    _check_gradients("short", grads, ct.backward(ref, g64), 5e-5)
+
+
+def test_long_config_every_chain(cufk, device):
+    """The long-chain bench configuration (B = 64, N = 131075, float32, random anchors: 64
+    segments of 2048 steps per chain), every chain.  Coordinates: the single-workgroup bars
+    scaled with the chain length, as for every long chain (1e-5 nm RMS and 1e-4 nm max-abs per
+    2049 points: 6.4e-4 and 6.4e-3 nm here; the float scan's rounding drifts along the chain).
+    The internal-coordinate round trip holds at the chain's own rounding scale, which the drift
+    does not enter: each bond, angle and dihedral is placed by one segment's float transform.
+    Gradients: within 5e-5 per chain of the float64 adjoint over the float64 chain, the
+    single-workgroup bar (the backward runs the position-based adjoint over each segment's
+    local positions, which stay within the segment's extent of its origin)."""
+    B, N = 64, 131075
+    L, A, D, g, p0, fd, n0 = _synthetic(B, N, 6, device)
+    f32 = [t.float() for t in (L, A, D, g, p0, fd, n0)]
+    Lf, Af, Df = (t.clone().requires_grad_(True) for t in f32[:3])
+    xyz = cufk.reconstruct_long(Lf, Af, Df, *f32[4:])
+    grads = torch.autograd.grad(xyz, (Lf, Af, Df), f32[3])
+    L64, A64, D64, g64 = (t.double() for t in f32[:4])
+    ref = ct.forward(L64, A64, D64, *(t.double() for t in f32[4:]))
+    diff = xyz.detach().double() - ref
+    rms = float(diff.pow(2).sum(-1).mean().sqrt())
+    mx = diff.abs().amax(dim=(1, 2))
+    scale = N / 2049
+    print(f"long every chain: RMS {rms:.2e} nm over the batch, worst max-abs {mx.max():.2e} nm "
+          f"(bars {1e-5 * scale:.1e}, {1e-4 * scale:.1e}), extent {ref.abs().max():.0f} nm")
+    assert rms <= 1e-5 * scale and bool((mx <= 1e-4 * scale).all())
+    _check_roundtrip(xyz.detach(), L64, A64, D64, "long")
+    _check_gradients("long", grads, ct.backward(ref, g64), 5e-5)
 
 
 # ----------------------------------------------------------------- fused losses, every chain
