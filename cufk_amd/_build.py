@@ -32,12 +32,15 @@ EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 EXT_LIB = PKG / f"_C{EXT_SUFFIX}"
 
 # Every HIP translation unit is built with packed FP32 disabled: the compiler must not emit
-# v_pk_{add,mul,fma}_f32.
+# v_pk_{add,mul,fma}_f32.  A pointer passed where a more strictly aligned type is expected is
+# an error: rows sit at any element offset, so only the element-aligned vector types may touch
+# them.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++20",
     "-fPIC",
+    "-Werror=align-mismatch",
     "-Xclang",
     "-target-feature",
     "-Xclang",

@@ -42,6 +42,21 @@ template <bool Stream, typename V> __device__ __forceinline__ void global_store(
   else
     *p = v;
 }
+// The element-aligned vectors take overloads of their own: deducing V from an f32x4u* would
+// drop the typedef's alignment and store through a 16-byte-aligned vector type, which rows at
+// any float offset are not.
+template <bool Stream> __device__ __forceinline__ void global_store(f32x4u* p, f32x4u v) {
+  if constexpr (Stream)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
+}
+template <bool Stream> __device__ __forceinline__ void global_store(f64x2u* p, f64x2u v) {
+  if constexpr (Stream)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
+}
 
 template <int W, int K, int Pad = 4> struct Layout {
   static_assert(K % 4 == 0, "lane segments must be whole 16-byte groups");
