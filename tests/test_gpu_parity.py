@@ -139,6 +139,53 @@ def test_empty_batch(cufk, device):
     assert xyz.shape == (0, 10, 3)
 
 
+def _empty_rows(N, dtype, device):
+    return [torch.zeros(0, N - k, device=device, dtype=dtype, requires_grad=True) for k in (1, 2, 3)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["reconstruct", "anchor_grads", "long", "loss", "rmsd"])
+def test_empty_batch_every_entry_point(cufk, device, dtype, kind):
+    """B = 0 through every reconstruct entry point, forward and backward: empty outputs and
+    gradients of the inputs' shapes (anchor gradients zero), no launch of an empty grid."""
+    N = 40
+    L, A, D = _empty_rows(N, dtype, device)
+    an = [torch.tensor(v, device=device, dtype=dtype, requires_grad=kind == "anchor_grads")
+          for v in ((0.1, 0.2, 0.3), (1.0, 0.0, 0.0), (0.0, 1.0, 0.0))]
+    target = torch.zeros(0, N, 3, device=device, dtype=dtype)
+    if kind == "reconstruct":
+        out = cufk.reconstruct(L, A, D, *an)
+    elif kind == "anchor_grads":
+        out = cufk.reconstruct(L, A, D, *an, anchor_grads=True)
+    elif kind == "long":
+        out = cufk.reconstruct_long(L, A, D, *an, segment_steps=16)
+    elif kind == "loss":
+        out = cufk.reconstruct_loss(L, A, D, target, *an)
+    else:
+        out = cufk.reconstruct_rmsd(L, A, D, target, *an)
+    assert out.shape == ((0, N, 3) if kind in ("reconstruct", "anchor_grads", "long") else (0,))
+    inputs = (L, A, D, *an) if kind == "anchor_grads" else (L, A, D)
+    grads = torch.autograd.grad(out, inputs, torch.zeros_like(out))
+    for g, x in zip(grads, inputs):
+        assert g.shape == x.shape
+    if kind == "anchor_grads":
+        assert all(bool((g == 0).all()) for g in grads[3:])
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("kind", ["apply", "loss", "rmsd"])
+def test_empty_batch_torsion(cufk, device, kind):
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    N = 40
+    raw = torch.zeros(0, 2 * (N - 3), device=device, requires_grad=True)
+    target = torch.zeros(0, N, 3, device=device)
+    out = f(raw) if kind == "apply" else (f.loss(raw, target) if kind == "loss" else f.rmsd(raw, target))
+    assert out.shape == ((0, N, 3) if kind == "apply" else (0,))
+    (g,) = torch.autograd.grad(out, (raw,), torch.zeros_like(out))
+    assert g.shape == raw.shape
+    torch.cuda.synchronize()
+
+
 # ----------------------------------------------------------------- backward
 
 
