@@ -173,6 +173,33 @@ def test_empty_batch_every_entry_point(cufk, device, dtype, kind):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+def test_partial_requires_grad_and_no_grad_mode(cufk, device, dtype):
+    """Every subset of (lengths, angles, dihedrals) requiring grad gets the gradients of the
+    full run, bit for bit; the others get none.  Under torch.no_grad (and with no input
+    requiring grad) the output needs no graph and equals the autograd forward's bit for bit
+    (the flagged and plain forwards place points with the same arithmetic)."""
+    d = _inputs(5, 300, seed=41, anchors=True, dtype=dtype)
+    xyz_full, full = _run(cufk, d, dtype, device)
+    an = _anchor_tensors(d, dtype, device)
+    g = _dev(d["grad"], dtype, device)
+    for mask in range(1, 8):
+        wants = [bool(mask >> k & 1) for k in range(3)]
+        L, A, D = (_dev(d[k], dtype, device, w) for k, w in zip(("lengths", "angles", "dihedrals"), wants))
+        xyz = cufk.reconstruct(L, A, D, **an)
+        picked = [t for t, w in zip((L, A, D), wants) if w]
+        grads = torch.autograd.grad(xyz, picked, g)
+        for got, want in zip(grads, [f for f, w in zip(full, wants) if w]):
+            assert torch.equal(got, want), mask
+    with torch.no_grad():
+        L, A, D = (_dev(d[k], dtype, device, True) for k in ("lengths", "angles", "dihedrals"))
+        plain = cufk.reconstruct(L, A, D, **an)
+    assert not plain.requires_grad and torch.equal(plain, xyz_full.detach())
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    plain = cufk.reconstruct(L, A, D, **an)
+    assert not plain.requires_grad and torch.equal(plain, xyz_full.detach())
+
+
 @pytest.mark.parametrize("kind", ["apply", "loss", "rmsd"])
 def test_empty_batch_torsion(cufk, device, kind):
     f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
