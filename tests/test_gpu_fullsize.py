@@ -10,6 +10,8 @@ NeRF forward and the explicit world-frame reverse adjoint.  Bars:
   device: bond lengths, bond angles and dihedrals recovered from the stored coordinates agree
   with the inputs within what float32 rounding at the chain's extent allows (derived in
   `_check_roundtrip`);
+* float64 at the C2 and C3 shapes: coordinates within 1e-12 nm and gradients within 1e-10
+  relative on every chain;
 * float16/bfloat16 (C4): reported, held to sanity bounds;
 * the extension bench configurations, short chains (131072 x 64) and long chains (64 x 131075),
   every chain: coordinates, round trip and gradients (derived in the tests);
@@ -139,6 +141,44 @@ def test_config2_every_chain(cufk, device):
         err = _per_chain_rel(got, w)
         print(f"C2 every chain d/d{name}: worst per-chain rel err {err.max():.2e} (chain {int(err.argmax())})")
         assert bool((err <= 5e-5).all())
+
+
+def test_config2_fp64_every_chain(cufk, device):
+    """The C2 shape in float64 (B = 4096, N = 2049, random anchors), every chain: coordinates
+    within 1e-12 nm of the serial float64 walk (the lane scans, wave scans and carries of the
+    kernel associate the same products differently, a few 1e-14 at this extent), gradients
+    within 1e-10 relative per chain of the float64 adjoint."""
+    B, N = 4096, 2049
+    L, A, D, g, p0, fd, n0 = _synthetic(B, N, 22, device)
+    Lr, Ar, Dr = (t.clone().requires_grad_(True) for t in (L, A, D))
+    xyz = cufk.reconstruct(Lr, Ar, Dr, p0, fd, n0)
+    grads = torch.autograd.grad(xyz, (Lr, Ar, Dr), g)
+    ref = ct.forward(L, A, D, p0, fd, n0)
+    err = (xyz.detach() - ref).abs().amax(dim=(1, 2))
+    print(f"C2 fp64 every chain: worst max-abs {err.max():.2e} nm (chain {int(err.argmax())})")
+    assert bool((err <= 1e-12).all())
+    _check_gradients("C2 fp64", grads, ct.backward(ref, g), 1e-10)
+
+
+def test_config3_fp64_every_chain(cufk, device):
+    """The C3 torsion shape in float64 (B = 8192, N = 771), every chain: coordinates within
+    1e-12 nm of the float64 torsion restatement, raw-pair gradients within 1e-10 relative per
+    chain of its adjoint."""
+    B, N = 8192, 771
+    gen = torch.Generator().manual_seed(33)
+    raw64 = torch.randn(B, 2 * (N - 3), generator=gen, dtype=torch.float64).to(device)
+    g64 = torch.randn(B, N, 3, generator=gen, dtype=torch.float64).to(device)
+    c = o.torsion_constants(BOND_LENGTHS, BOND_ANGLES)
+    raw = raw64.clone().requires_grad_(True)
+    xyz = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)(raw)
+    (graw,) = torch.autograd.grad(xyz, (raw,), g64)
+    ref = ct.torsion_forward(raw64, c.lengths, c.sin, c.cos)
+    err = (xyz.detach() - ref).abs().amax(dim=(1, 2))
+    print(f"C3 fp64 every chain: worst max-abs {err.max():.2e} nm (chain {int(err.argmax())})")
+    assert bool((err <= 1e-12).all())
+    gerr = _per_chain_rel(graw, ct.torsion_backward(raw64, ref, g64, c.lengths))
+    print(f"C3 fp64 every chain d/draw: worst per-chain rel err {gerr.max():.2e}")
+    assert bool((gerr <= 1e-10).all())
 
 
 def test_config3_every_chain(cufk, device):
