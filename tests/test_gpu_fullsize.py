@@ -146,7 +146,7 @@ def test_config2_every_chain(cufk, device):
 def test_config2_fp64_every_chain(cufk, device):
     """The C2 shape in float64 (B = 4096, N = 2049, random anchors), every chain: coordinates
     within 1e-12 nm of the serial float64 walk (the lane scans, wave scans and carries of the
-    kernel associate the same products differently, a few 1e-14 at this extent), gradients
+    kernel associate the same products differently, about 1e-13 at this extent), gradients
     within 1e-10 relative per chain of the float64 adjoint."""
     B, N = 4096, 2049
     L, A, D, g, p0, fd, n0 = _synthetic(B, N, 22, device)
