@@ -36,7 +36,7 @@ over the chains with torch's intra-op threads, the median of 3 runs over the con
 a subset of it where one run would take longer than about 20 s), scaled to atoms/s.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss] [--graph]
+                    [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss|rmsd|torsion_loss] [--graph]
 
 With --graph each input set's step is captured once in a HIP graph (torch.cuda.graph) and the
 timed steps replay the graphs: the kernels are the same, the per-step Python, autograd-engine and

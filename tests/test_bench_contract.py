@@ -1,0 +1,72 @@
+"""bench.py's contract pieces that need no GPU: the single-GPU refusal, the configurations, and
+the measured-traffic table it reports as roofline.traffic, checked against the committed
+rocprofv3 summary and against the algorithmic byte counts that summary lists."""
+
+from __future__ import annotations
+
+import importlib.util
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_module", ROOT / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_more_than_one_gpu_is_refused():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2", "--steps", "1", "--warmup", "0"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stdout + proc.stderr
+
+
+def test_headline_config_is_the_baseline_metric():
+    b = _bench()
+    assert b.CONFIGS["c2"] == ("reconstruct", "float32", 4096, 2049)
+    assert b.CONFIGS["c1"] == ("reconstruct", "float32", 1024, 384)
+    assert b.CONFIGS["c3"] == ("torsion", "float32", 8192, 771)
+    assert b.CONFIGS["c4_bf16"] == ("reconstruct", "bfloat16", 16384, 1026)
+
+
+def _traffic_rows():
+    text = (ROOT / "profiles" / "hbm_traffic_c2_c3_c4.md").read_text()
+    rows = {}
+    for m in re.finditer(r"^\| (c2|c3|c4_bf16) \| ([^|]+) \|[^|]+\|[^|]+\| ([\d,]+) \| ([\d,]+) \| ([\d,]+) \| ([\d,]+) = ",
+                         text, re.M):
+        cfg, kernel = m.group(1), m.group(2).strip()
+        read, write, total, algorithmic = (int(m.group(k).replace(",", "")) for k in (3, 4, 5, 6))
+        rows.setdefault(cfg, []).append((kernel, read, write, total, algorithmic))
+    per_step = {m.group(1): int(m.group(2).replace(",", ""))
+                for m in re.finditer(r"(c2|c3|c4_bf16) ([\d,]+) B", text)}
+    return rows, per_step
+
+
+def test_measured_traffic_matches_the_committed_profile():
+    b = _bench()
+    rows, per_step = _traffic_rows()
+    assert set(rows) == set(b.MEASURED_TRAFFIC) == set(per_step)
+    for cfg, kernels in rows.items():
+        assert len(kernels) == 2, cfg  # forward and backward
+        for _, read, write, total, _ in kernels:
+            assert read + write == total
+        assert sum(k[3] for k in kernels) == b.MEASURED_TRAFFIC[cfg] == per_step[cfg], cfg
+
+
+def test_profile_algorithmic_bytes_follow_the_formulas():
+    """The summary's algorithmic column: forward s(6N-6) and backward s(9N-12) bytes per chain
+    for reconstruct, s(5N-6) and s(10N-12) for torsion (s the element size)."""
+    b = _bench()
+    rows, _ = _traffic_rows()
+    size = {"float32": 4, "bfloat16": 2}
+    for cfg, kernels in rows.items():
+        kind, dtype, B, N = b.CONFIGS[cfg]
+        s = size[dtype]
+        fwd, bwd = ((5 * N - 6), (10 * N - 12)) if kind == "torsion" else ((6 * N - 6), (9 * N - 12))
+        assert [k[4] for k in kernels] == [s * B * fwd, s * B * bwd], cfg
