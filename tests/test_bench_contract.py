@@ -70,3 +70,15 @@ def test_profile_algorithmic_bytes_follow_the_formulas():
         s = size[dtype]
         fwd, bwd = ((5 * N - 6), (10 * N - 12)) if kind == "torsion" else ((6 * N - 6), (9 * N - 12))
         assert [k[4] for k in kernels] == [s * B * fwd, s * B * bwd], cfg
+
+
+def test_c2_trace_recomputes_the_stated_roofline_fraction():
+    """profiles/reconstruct_c2_kernel_stats.md: the two kernels' average durations give the step
+    fraction it states (algorithmic bytes / (forward + backward) / 8 TB/s)."""
+    text = (ROOT / "profiles" / "reconstruct_c2_kernel_stats.md").read_text()
+    avg = {m.group(1): int(m.group(2)) for m in re.finditer(r"^\| (reconstruct_\w+) \| \d+ \| (\d+) \|", text, re.M)}
+    step_ns = avg["reconstruct_forward_kernel"] + avg["reconstruct_backward_saved_kernel"]
+    B, N = 4096, 2049
+    frac = 4 * B * (15 * N - 18) / (step_ns * 1e-9) / 8e12
+    stated = float(re.search(r"\*\*(0\.\d+)\*\* of 8 TB/s", text).group(1))
+    assert abs(frac - stated) <= 0.0015, (frac, stated)
