@@ -96,3 +96,43 @@ def test_torsion_step_replays(device):
         torch.cuda.synchronize()
         for got, want in zip(out, ref):
             assert torch.equal(got, want), rep
+
+
+@pytest.mark.parametrize("kind", ["loss", "rmsd", "long", "anchor_grads"])
+def test_extension_steps_replay(device, kind):
+    """The fused coordinate loss and RMSD, long chains (several segments, so every long-chain
+    pass is in the graph) and anchor gradients: captured and replayed as the plain step."""
+    import cufk_amd
+
+    B, N = (6, 3000) if kind == "long" else (64, 700)
+    s = _set(B, N, 12, torch.float32, device)
+    names = ("lengths", "angles", "dihedrals", "p0", "first_direction", "initial_normal")
+    grad_anchors = kind == "anchor_grads"
+    ins = [s[k].clone().requires_grad_(i < 3 or grad_anchors) for i, k in enumerate(names)]
+    extra = s["grad"].clone()  # the target of the losses, the upstream gradient otherwise
+
+    def step(L, A, D, p0, fd, n0, extra):
+        if kind == "loss":
+            out = cufk_amd.reconstruct_loss(L, A, D, extra, p0, fd, n0)
+        elif kind == "rmsd":
+            out = cufk_amd.reconstruct_rmsd(L, A, D, extra, p0, fd, n0)
+        elif kind == "long":
+            out = cufk_amd.reconstruct_long(L, A, D, p0, fd, n0, segment_steps=512)
+        else:
+            out = cufk_amd.reconstruct(L, A, D, p0, fd, n0, anchor_grads=True)
+        upstream = torch.ones_like(out) if kind in ("loss", "rmsd") else extra
+        wrt = (L, A, D, p0, fd, n0) if grad_anchors else (L, A, D)
+        return (out, *torch.autograd.grad(out, wrt, upstream))
+
+    graph, out = _capture(step, (*ins, extra))
+    for rep in range(4):
+        t = _set(B, N, 200 + rep, torch.float32, device)
+        with torch.no_grad():
+            for dst, k in zip(ins, names):
+                dst.copy_(t[k])
+            extra.copy_(t["grad"])
+        graph.replay()
+        ref = step(*(t[k].clone().requires_grad_(i < 3 or grad_anchors) for i, k in enumerate(names)), t["grad"].clone())
+        torch.cuda.synchronize()
+        for got, want in zip(out, ref):
+            assert torch.equal(got, want), (kind, rep)
