@@ -466,6 +466,59 @@ def test_deterministic_and_stream(cufk, device):
         assert torch.equal(a, b)
 
 
+def test_concurrent_streams(cufk, device):
+    """Four different workloads enqueued on four streams with no synchronisation between them
+    (reconstruct with default anchors, torsion, long chains, the fused RMSD), forward and
+    backward, three times over: each equals its sequential result bit for bit.  The library
+    holds no state between calls that they could share, beyond read-only defaults."""
+    head = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    rng = np.random.default_rng(19)
+    d1 = _inputs(32, 900, seed=91, anchors=False, dtype=torch.float32)
+    d2 = _inputs(8, 5000, seed=92, anchors=True, dtype=torch.float32)
+    d3 = _inputs(48, 700, seed=93, anchors=True, dtype=torch.float32)
+    raw = torch.as_tensor(rng.normal(size=(64, 2 * 400)), dtype=torch.float32, device=device)
+    graw = torch.as_tensor(rng.normal(size=(64, 403, 3)), dtype=torch.float32, device=device)
+    target = _dev(d3["grad"], torch.float32, device)
+
+    def rows(d):
+        return [_dev(d[k], torch.float32, device, True) for k in ("lengths", "angles", "dihedrals")]
+
+    def w1():
+        L, A, D = rows(d1)
+        x = cufk.reconstruct(L, A, D)
+        return (x, *torch.autograd.grad(x, (L, A, D), _dev(d1["grad"], torch.float32, device)))
+
+    def w2():
+        r = raw.clone().requires_grad_(True)
+        x = head(r)
+        return (x, *torch.autograd.grad(x, (r,), graw))
+
+    def w3():
+        L, A, D = rows(d2)
+        x = cufk.reconstruct_long(L, A, D, **_anchor_tensors(d2, torch.float32, device), segment_steps=700)
+        return (x, *torch.autograd.grad(x, (L, A, D), _dev(d2["grad"], torch.float32, device)))
+
+    def w4():
+        L, A, D = rows(d3)
+        loss = cufk.reconstruct_rmsd(L, A, D, target, **_anchor_tensors(d3, torch.float32, device))
+        return (loss, *torch.autograd.grad(loss.sum(), (L, A, D)))
+
+    work = (w1, w2, w3, w4)
+    want = [w() for w in work]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in work]
+    for rep in range(3):
+        got = []
+        for s, w in zip(streams, work):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                got.append(w())
+        torch.cuda.synchronize()
+        for i, (g, ww) in enumerate(zip(got, want)):
+            for a, b in zip(g, ww):
+                assert torch.equal(a, b), (rep, i)
+
+
 def test_full_size_config2_sampled(cufk, device):
     # B = 4096, N = 2049 fp32: compare 6 sampled chains with the float64 oracle.
     B, N = 4096, 2049
