@@ -56,3 +56,33 @@ def test_batches_past_two_to_the_31_elements(device, B, N):
         assert (err <= 5e-5).all()
     del xyz, grads, L, A, D, g, Lr, Ar, Dr
     torch.cuda.empty_cache()
+
+
+def test_torsion_batch_past_two_to_the_31_elements(device):
+    """The torsion path at 8M chains of 100 points (raw pairs with their row stride, xyz past
+    2^31 elements; about 32 GB)."""
+    import cufk_amd
+
+    bond_lengths = (0.14685231, 0.15365194, 0.13405086)
+    bond_angles = (1.9676635, 2.062335, 2.164016)
+    B, N = 8_000_000, 100
+    assert B * N * 3 > 2**31
+    gen = torch.Generator(device=device).manual_seed(7)
+    raw = torch.randn(B, 2 * (N - 3), generator=gen, device=device).requires_grad_(True)
+    g = torch.randn(B, N, 3, generator=gen, device=device)
+    xyz = cufk_amd.compile_torsion(bond_lengths, bond_angles)(raw)
+    (graw,) = torch.autograd.grad(xyz, (raw,), g)
+    torch.cuda.synchronize()
+    edge = 2**31 // (3 * N)
+    rows = [0, edge - 1, edge, edge + 1, B - 1]
+    c = o.torsion_constants(bond_lengths, bond_angles)
+    pick = lambda t: t.detach()[rows].double().cpu().numpy()  # noqa: E731
+    ref = o.torsion_forward(pick(raw), c)
+    ref_g = o.torsion_backward(pick(raw), ref, pick(g), c)
+    diff = pick(xyz) - ref
+    rms = np.sqrt(np.mean(np.sum(diff**2, axis=-1), axis=1))
+    err = np.abs(pick(graw) - ref_g).max(axis=1) / np.abs(ref_g).max(axis=1)
+    print(f"torsion B={B} N={N}: chains {rows}: RMS {rms}, max-abs {np.abs(diff).max():.2e}, grad rel {err}")
+    assert (rms <= 1e-5).all() and np.abs(diff).max() <= 1e-4 and (err <= 5e-5).all()
+    del xyz, graw, raw, g
+    torch.cuda.empty_cache()
