@@ -287,3 +287,41 @@ def test_fused_loss_status_paths(lib):
     assert tb(0, 1, p, 10, p, p, null, null, p, 10, p, 4, 8, null) == ERR_NULL
     assert tb(0, 0, p, 10, p, p, null, null, p, -2, p, 4, 8, null) == ERR_STRIDE
     assert lib.cufk_error_string(ERR_LOSS) == b"unknown or unsupported loss kind"
+
+
+def declared_parameter_counts():
+    text = HEADER.read_text()
+    counts = {}
+    for m in re.finditer(r"^\s*(?:int|int64_t|const char\*)\s+(cufk_\w+)\s*\((.*?)\);", text, re.M | re.S):
+        params = m.group(2).strip()
+        counts[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return counts
+
+
+def _documented_argtypes():
+    """The `lib.NAME.argtypes = [...]` lines of INTEGRATION.md, evaluated with placeholders."""
+    import types
+
+    ns = {"vp": "p", "i64": "i", "ctypes": types.SimpleNamespace(c_int="c", c_void_p="p", c_int64="i")}
+    out = {}
+    for m in re.finditer(r"^lib\.(cufk_\w+)\.argtypes = (.+)$", (ROOT / "INTEGRATION.md").read_text(), re.M):
+        out[m.group(1)] = eval(m.group(2), {}, dict(ns))  # noqa: S307 - the repository's own documentation
+    return out
+
+
+def test_documented_ctypes_bindings_match_the_header():
+    """Every argtypes list INTEGRATION.md gives has as many entries as the header's declaration
+    has parameters (a count that has drifted once is now pinned)."""
+    declared = declared_parameter_counts()
+    documented = _documented_argtypes()
+    assert len(documented) >= 10
+    for name, types_ in documented.items():
+        assert len(types_) == declared[name], (name, len(types_), declared[name])
+
+
+def test_test_bindings_match_the_header(lib):
+    declared = declared_parameter_counts()
+    for name, n in declared.items():
+        fn = getattr(lib, name)
+        if fn.argtypes is not None:
+            assert len(fn.argtypes) == n, (name, len(fn.argtypes), n)
