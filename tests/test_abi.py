@@ -325,3 +325,23 @@ def test_test_bindings_match_the_header(lib):
         fn = getattr(lib, name)
         if fn.argtypes is not None:
             assert len(fn.argtypes) == n, (name, len(fn.argtypes), n)
+
+
+def test_documented_c_snippet_compiles(tmp_path):
+    """The C example of the integration notes, wrapped in a function, compiles against the
+    header with gcc (syntax and types only; nothing is linked or run)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no host C compiler")
+    body = re.search(r"```c\n(.*?)```", (ROOT / "INTEGRATION.md").read_text(), re.S).group(1)
+    include, rest = body.split("\n", 1)
+    src = tmp_path / "snippet.c"
+    src.write_text("#include <math.h>\n#include <stdint.h>\n#include <stdio.h>\n" + include + "\n"
+                   "int demo(const void* d_raw, int64_t raw_stride, void* d_xyz, int64_t B, int64_t N, void* stream) {\n"
+                   + rest + "\nreturn rc;\n}\n")
+    proc = subprocess.run([gcc, "-std=c11", "-Wall", "-Werror", "-fsyntax-only", f"-I{ROOT / 'include'}", str(src)],
+                          capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr
