@@ -615,6 +615,44 @@ __device__ __forceinline__ Rigid<float> wave_prefix(Rigid<float> x) {
   CUFK_RIGID_DPP_LEVEL("row_bcast:31 row_mask:0xc bank_mask:0xf", o, x);
   return x;
 }
+// Inclusive ordered product over each aligned group of G lanes (G a power of two <= 16, so a
+// group lies inside one 16-lane DPP row; t = lane % G): wave_prefix's row_shr levels below G.
+// A level's DPP source must stay active in EXEC (a disabled source lane reads as out of
+// range), so lanes whose source lies in the previous group (t < D) are restored to their own
+// transform afterwards, one select per entry; at D = 4 in groups of 8 those lanes are banks 0
+// and 2 of each row, which bank_mask leaves unwritten instead.  With G = 16 the row bound
+// already excludes them.
+template <int G> __device__ __forceinline__ Rigid<float> group_prefix(Rigid<float> x, int t) {
+  static_assert(G >= 1 && G <= 16 && (G & (G - 1)) == 0, "groups are powers of two inside one DPP row");
+  Rigid<float> o;
+  auto keep_own = [&](bool own) {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) o.m[i] = own ? x.m[i] : o.m[i];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) o.v[i] = own ? x.v[i] : o.v[i];
+  };
+  if constexpr (G >= 2) {
+    CUFK_RIGID_DPP_LEVEL("row_shr:1 row_mask:0xf bank_mask:0xf", x, o);
+    if constexpr (G < 16) keep_own(t < 1);
+    x = o;
+  }
+  if constexpr (G >= 4) {
+    CUFK_RIGID_DPP_LEVEL("row_shr:2 row_mask:0xf bank_mask:0xf", x, o);
+    if constexpr (G < 16) keep_own(t < 2);
+    x = o;
+  }
+  if constexpr (G == 8) {
+    CUFK_RIGID_DPP_LEVEL("row_shr:4 row_mask:0xf bank_mask:0xa", x, o);
+    x = o;
+  } else if constexpr (G == 16) {
+    CUFK_RIGID_DPP_LEVEL("row_shr:4 row_mask:0xf bank_mask:0xf", x, o);
+    x = o;
+    CUFK_RIGID_DPP_LEVEL("row_shr:8 row_mask:0xf bank_mask:0xf", x, o);
+    x = o;
+  }
+  return x;
+}
+
 #undef CUFK_RIGID_DPP_LEVEL
 
 // OR of a predicate over the workgroup: one vote per wave into flags[], then a barrier.

@@ -42,6 +42,24 @@ template <int G, typename R> __device__ __forceinline__ Rigid<R> group_exclusive
   const int t = lane & (G - 1);
   if constexpr (G == 1) {
     return rigid_identity<R>();
+  } else if constexpr (std::is_same_v<R, float>) {
+    // The fused DPP levels (group_prefix: 51 VALU issues and at most 12 selects per level,
+    // against about 75 for the rounds below), then the shift by one lane: mov_dpp needs no
+    // old value, since every lane without a source (a row start) is a group start and takes
+    // the identity.
+    x = group_prefix<G>(x, t);
+    Rigid<R> y;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const R v = __builtin_bit_cast(R, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x.m[i]), kRowShr1, 0xf, 0xf, true));
+      y.m[i] = t == 0 ? ((i % 4 == 0) ? R(1) : R(0)) : v;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const R v = __builtin_bit_cast(R, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x.v[i]), kRowShr1, 0xf, 0xf, true));
+      y.v[i] = t == 0 ? R(0) : v;
+    }
+    return y;
   } else {
     x = group_scan_round<kRowShr1, 1, G>(x, t);
     if constexpr (G >= 4) x = group_scan_round<kRowShr2, 2, G>(x, t);
@@ -127,27 +145,28 @@ constexpr int flat_windows(int elems, int elem_bytes, int lanes) {
   const int e = 16 / elem_bytes;
   return ((elems + 2 * e - 2) / e + lanes - 1) / lanes;
 }
-// fslot<Gap>(f0 + k) for 0 <= k < E: a shift per element for a power-of-two Gap, else from one
-// division (q = f0 / Gap, f0 % Gap) per window.
+// fslot<Gap>(f0 + k) for 0 <= k < 2 Gap: a shift per element for a power-of-two Gap, else from
+// one division per run (q = f0 / Gap, off = f0 % Gap, unsigned so that the compiler knows
+// off < Gap and drops the compare that cannot hold for a constant k).
 template <int Gap> struct FlatRun {
   static constexpr bool kPow2 = (Gap & (Gap - 1)) == 0;
-  int base;  // f0 for a power-of-two Gap, else fslot(f0) = f0 + q
-  int off;   // f0 % Gap (unused for a power-of-two Gap)
+  int base;      // f0 for a power-of-two Gap, else fslot(f0) = f0 + q
+  unsigned off;  // f0 % Gap (unused for a power-of-two Gap)
   __device__ __forceinline__ explicit FlatRun(int f0) {
     if constexpr (kPow2) {
       base = f0;
       off = 0;
     } else {
-      const int q = f0 / Gap;
-      base = f0 + q;
-      off = f0 - q * Gap;
+      const unsigned u = static_cast<unsigned>(f0);
+      base = f0 + static_cast<int>(u / Gap);
+      off = u % Gap;
     }
   }
   __device__ __forceinline__ int slot(int k) const {
     if constexpr (kPow2)
       return fslot<Gap>(base + k);
     else
-      return base + k + (off + k >= Gap ? 1 : 0);
+      return base + k + (off + k >= Gap ? 1 : 0) + (off + k >= 2 * Gap ? 1 : 0);
   }
 };
 
@@ -386,26 +405,29 @@ __global__ __launch_bounds__(64 * W) void packed_forward_kernel(
         gm[3 * r + cc] = F[3 * r] * excl.m[cc] + F[3 * r + 1] * excl.m[3 + cc] + F[3 * r + 2] * excl.m[6 + cc];
     }
     const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
-    const int e0 = ln.c * 3 * points + 9 + 3 * ln.s0;
+    const FlatRun<P::kPointGap> run(ln.c * 3 * points + 9 + 3 * ln.s0);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
       if (i < ln.count) {
-        const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
-        stage[fslot<P::kPointGap>(e0 + 3 * i)] = x.x;
-        stage[fslot<P::kPointGap>(e0 + 3 * i + 1)] = x.y;
-        stage[fslot<P::kPointGap>(e0 + 3 * i + 2)] = x.z;
+        // gv as the addend of the first fma: three issues per coordinate, not four.
+        const V3<R> x = {fma(gm[2], y[i][2], fma(gm[1], y[i][1], fma(gm[0], y[i][0], gv.x))),
+                         fma(gm[5], y[i][2], fma(gm[4], y[i][1], fma(gm[3], y[i][0], gv.y))),
+                         fma(gm[8], y[i][2], fma(gm[7], y[i][1], fma(gm[6], y[i][0], gv.z)))};
+        stage[run.slot(3 * i)] = x.x;
+        stage[run.slot(3 * i + 1)] = x.y;
+        stage[run.slot(3 * i + 2)] = x.z;
         xmax = abs_max3(xmax, x);
       }
     }
   }
   if (ln.leader) {
     const V3<R> h[3] = {ff.p0, ff.p1, ff.p2};
-    const int e0 = ln.c * 3 * points;
+    const FlatRun<P::kPointGap> run(ln.c * 3 * points);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      stage[fslot<P::kPointGap>(e0 + 3 * j)] = h[j].x;
-      stage[fslot<P::kPointGap>(e0 + 3 * j + 1)] = h[j].y;
-      stage[fslot<P::kPointGap>(e0 + 3 * j + 2)] = h[j].z;
+      stage[run.slot(3 * j)] = h[j].x;
+      stage[run.slot(3 * j + 1)] = h[j].y;
+      stage[run.slot(3 * j + 2)] = h[j].z;
     }
   }
   if constexpr (FastPath<T>::kEnabled) {
@@ -444,14 +466,16 @@ __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, 
                                                         LaneGrads<compute_t<T>, K>& out, double* anchor) {
   using R = compute_t<T>;
   const int last = ln.count - 1;
-  const int e0 = ln.c * 3 * points + 3 * ln.s0;  // point s0: the three points before the lane's run, then the run
+  static_assert(3 * K + 9 <= 2 * P::kPointGap, "a lane's run crosses at most two pad words");
+  // Point s0: the three points before the lane's run, then the run.
+  const FlatRun<P::kPointGap> run(ln.c * 3 * points + 3 * ln.s0);
+  const FlatRun<P::kPointGap> chain(ln.c * 3 * points);  // the chain's points 0..2
   R xr[3 * K + 9], gr[3 * K];
 #pragma unroll
-  for (int i = 0; i < 3 * K + 9; ++i) xr[i] = xs[fslot<P::kPointGap>(e0 + i)];
+  for (int i = 0; i < 3 * K + 9; ++i) xr[i] = xs[run.slot(i)];
 #pragma unroll
-  for (int i = 0; i < 3 * K; ++i) gr[i] = gs[fslot<P::kPointGap>(e0 + 9 + i)];
-  const int ec = ln.c * 3 * points + 6;
-  const V3<R> ctr = {xs[fslot<P::kPointGap>(ec)], xs[fslot<P::kPointGap>(ec + 1)], xs[fslot<P::kPointGap>(ec + 2)]};
+  for (int i = 0; i < 3 * K; ++i) gr[i] = gs[run.slot(9 + i)];
+  const V3<R> ctr = {xs[chain.slot(6)], xs[chain.slot(7)], xs[chain.slot(8)]};
   auto pos = [&](int j) { return V3<R>{xr[3 * j], xr[3 * j + 1], xr[3 * j + 2]} - ctr; };
 
   ForceMoment<R> lane_sum = {{R(0), R(0), R(0)}, {R(0), R(0), R(0)}};
@@ -484,11 +508,10 @@ __device__ __forceinline__ void packed_position_adjoint(const compute_t<T>* xs, 
   }
   if (ln.leader) {  // s0 = 0: xr holds points 0, 1, 2 first
     const V3<R> x0 = pos(0), x1 = pos(1), x2 = pos(2);
-    const int eg = ln.c * 3 * points;
-    const V3<R> g1 = {gs[fslot<P::kPointGap>(eg + 3)], gs[fslot<P::kPointGap>(eg + 4)], gs[fslot<P::kPointGap>(eg + 5)]};
-    const V3<R> g2 = {gs[fslot<P::kPointGap>(eg + 6)], gs[fslot<P::kPointGap>(eg + 7)], gs[fslot<P::kPointGap>(eg + 8)]};
+    const V3<R> g1 = {gs[chain.slot(3)], gs[chain.slot(4)], gs[chain.slot(5)]};
+    const V3<R> g2 = {gs[chain.slot(6)], gs[chain.slot(7)], gs[chain.slot(8)]};
     if (anchor != nullptr) {
-      const V3<R> g0 = {gs[fslot<P::kPointGap>(eg)], gs[fslot<P::kPointGap>(eg + 1)], gs[fslot<P::kPointGap>(eg + 2)]};
+      const V3<R> g0 = {gs[chain.slot(0)], gs[chain.slot(1)], gs[chain.slot(2)]};
       store_anchor_sums(anchor, F, M, x0, x1, g0, g1, g2);
     }
     F = F + g2;
@@ -514,7 +537,7 @@ __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_
   const int el = ln.c * (points - 1) + 2 + ln.s0;
   const int ea = ln.c * (points - 2) + 1 + ln.s0;
   const int ed = ln.c * (points - 3) + ln.s0;
-  const int eg = ln.c * 3 * points + 9 + 3 * ln.s0;
+  const FlatRun<P::kPointGap> grun(ln.c * 3 * points + 9 + 3 * ln.s0);
 
   Rigid<double> qd = rigid_identity<double>();
   R Y[9];
@@ -530,8 +553,7 @@ __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_
         sin_cos_wide<Checked>(rows.A[fslot<P::kStepGap>(ea + i)], s, c);
         sin_cos_wide<Checked>(rows.D[fslot<P::kStepGap>(ed + i)], S, C);
         step_forward(qd.m, qd.v, static_cast<double>(l), s, c, S, C);
-        const V3<R> g = {gs[fslot<P::kPointGap>(eg + 3 * i)], gs[fslot<P::kPointGap>(eg + 3 * i + 1)],
-                         gs[fslot<P::kPointGap>(eg + 3 * i + 2)]};
+        const V3<R> g = {gs[grun.slot(3 * i)], gs[grun.slot(3 * i + 1)], gs[grun.slot(3 * i + 2)]};
         const R yv[3] = {static_cast<R>(qd.v[0]), static_cast<R>(qd.v[1]), static_cast<R>(qd.v[2])};
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -585,8 +607,7 @@ __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
       if (i < ln.count) {
-        const V3<R> g = {gs[fslot<P::kPointGap>(eg + 3 * i)], gs[fslot<P::kPointGap>(eg + 3 * i + 1)],
-                         gs[fslot<P::kPointGap>(eg + 3 * i + 2)]};
+        const V3<R> g = {gs[grun.slot(3 * i)], gs[grun.slot(3 * i + 1)], gs[grun.slot(3 * i + 2)]};
         Fs = Fs + g;
         Ms = Ms + cross(x, g);
         const R l = rows.L[fslot<P::kStepGap>(el + i)];
@@ -610,14 +631,14 @@ __device__ __forceinline__ void packed_exact_adjoint(const ParamRows<P, compute_
   else
     pass2.template operator()<false>();
   if (ln.leader) {
-    const int e = ln.c * 3 * points;
-    const V3<R> g1 = {gs[fslot<P::kPointGap>(e + 3)], gs[fslot<P::kPointGap>(e + 4)], gs[fslot<P::kPointGap>(e + 5)]};
-    const V3<R> g2 = {gs[fslot<P::kPointGap>(e + 6)], gs[fslot<P::kPointGap>(e + 7)], gs[fslot<P::kPointGap>(e + 8)]};
+    const FlatRun<P::kPointGap> chain(ln.c * 3 * points);
+    const V3<R> g1 = {gs[chain.slot(3)], gs[chain.slot(4)], gs[chain.slot(5)]};
+    const V3<R> g2 = {gs[chain.slot(6)], gs[chain.slot(7)], gs[chain.slot(8)]};
     const V3<R> F2 = Fs + g2;
     const V3<R> x1 = ff.p1 - ff.p2;
     const V3<R> tau2 = Ms - cross(x1, F2);
     if (anchor != nullptr) {
-      const V3<R> g0 = {gs[fslot<P::kPointGap>(e)], gs[fslot<P::kPointGap>(e + 1)], gs[fslot<P::kPointGap>(e + 2)]};
+      const V3<R> g0 = {gs[chain.slot(0)], gs[chain.slot(1)], gs[chain.slot(2)]};
       store_anchor_sums(anchor, Fs, Ms, ff.p0 - ff.p2, x1, g0, g1, g2);
     }
     out.head[0] = dot(ff.d0, F2 + g1);
@@ -726,24 +747,24 @@ __global__ __launch_bounds__(64 * W) void packed_backward_kernel(
     positions = !block_any<W>(irregular, vote, lane, wave);  // barrier: parameter reads retired
     if (positions) {
       if (ln.count > 0) {
-        const int e0 = ln.c * 3 * points + 9 + 3 * ln.s0;
+        const FlatRun<P::kPointGap> run(ln.c * 3 * points + 9 + 3 * ln.s0);
 #pragma unroll
         for (int i = 0; i < K; ++i) {
           if (i < ln.count) {
-            region_a[fslot<P::kPointGap>(e0 + 3 * i)] = x[i].x;
-            region_a[fslot<P::kPointGap>(e0 + 3 * i + 1)] = x[i].y;
-            region_a[fslot<P::kPointGap>(e0 + 3 * i + 2)] = x[i].z;
+            region_a[run.slot(3 * i)] = x[i].x;
+            region_a[run.slot(3 * i + 1)] = x[i].y;
+            region_a[run.slot(3 * i + 2)] = x[i].z;
           }
         }
       }
       if (ln.leader) {
         const V3<R> h[3] = {ff.p0 - ff.p2, ff.p1 - ff.p2, {R(0), R(0), R(0)}};
-        const int e0 = ln.c * 3 * points;
+        const FlatRun<P::kPointGap> run(ln.c * 3 * points);
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-          region_a[fslot<P::kPointGap>(e0 + 3 * j)] = h[j].x;
-          region_a[fslot<P::kPointGap>(e0 + 3 * j + 1)] = h[j].y;
-          region_a[fslot<P::kPointGap>(e0 + 3 * j + 2)] = h[j].z;
+          region_a[run.slot(3 * j)] = h[j].x;
+          region_a[run.slot(3 * j + 1)] = h[j].y;
+          region_a[run.slot(3 * j + 2)] = h[j].z;
         }
       }
     }
