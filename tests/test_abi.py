@@ -299,7 +299,7 @@ def declared_parameter_counts():
 
 
 def _documented_argtypes():
-    """The `lib.NAME.argtypes = [...]` lines of INTEGRATION.md, evaluated with placeholders."""
+    """The `lib.NAME.argtypes = [...]` lines of the integration notes, evaluated with placeholders."""
     import types
 
     ns = {"vp": "p", "i64": "i", "ctypes": types.SimpleNamespace(c_int="c", c_void_p="p", c_int64="i")}
@@ -310,8 +310,8 @@ def _documented_argtypes():
 
 
 def test_documented_ctypes_bindings_match_the_header():
-    """Every argtypes list INTEGRATION.md gives has as many entries as the header's declaration
-    has parameters (a count that has drifted once is now pinned)."""
+    """Every argtypes list the integration notes give has as many entries as the header's
+    declaration has parameters (a count that has drifted once is now pinned)."""
     declared = declared_parameter_counts()
     documented = _documented_argtypes()
     assert len(documented) >= 10
