@@ -696,6 +696,15 @@ template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up(const Ri
   for (int i = 0; i < 3; ++i) y.v[i] = dpp_move<kWaveShr1, 0xf>(R(0), x.v[i]);
   return y;
 }
+// Value of lane-1, and `first` in lane 0 (the same two moves per entry as wave_shift_up).
+template <typename R> __device__ __forceinline__ Rigid<R> wave_shift_up_from(const Rigid<R>& x, const Rigid<R>& first) {
+  Rigid<R> y;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) y.m[i] = dpp_move<kWaveShr1, 0xf>(first.m[i], x.m[i]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) y.v[i] = dpp_move<kWaveShr1, 0xf>(first.v[i], x.v[i]);
+  return y;
+}
 
 // Additive force/moment pair (torsion.cu:184-211).
 template <typename R> struct ForceMoment {
@@ -792,12 +801,15 @@ __device__ __forceinline__ Rigid<R> load_rigid(const R (&src)[W][12], int w) {
 
 // Exclusive prefix of the chain's rigid transforms before this lane's first step:
 // wave-level scan, then the totals of earlier waves (scan.cuh:63-101 restated for wave64).
+// Lane 0 of each wave starts from `first` (the identity unless the caller prepends a transform
+// to the chain: then wave 0 passes it and its lane 0 has already composed it into its total).
 // Contains one __syncthreads(); must be called by every thread of the workgroup.
 template <typename R, int W>
-__device__ __forceinline__ Rigid<R> lane_carry(const Rigid<R>& lane_total, R (&wave_total)[W][12], int lane, int wave) {
+__device__ __forceinline__ Rigid<R> lane_carry(const Rigid<R>& lane_total, R (&wave_total)[W][12], int lane, int wave,
+                                               const Rigid<R>& first = rigid_identity<R>()) {
   const Rigid<R> incl = wave_prefix(lane_total);
   if (lane == 63) store_rigid(wave_total, wave, incl);
-  Rigid<R> excl = wave_shift_up(incl, lane);
+  Rigid<R> excl = wave_shift_up_from(incl, first);
   __syncthreads();
   if constexpr (W > 1) {
     if (wave > 0) {

@@ -74,10 +74,11 @@ __global__ __launch_bounds__(64 * W) void long_forward_segments_kernel(
       p0, first_direction, initial_normal, out, flags + at, s.steps + 3, s.index == 0, state + at * kLongStateDoubles);
 }
 
-// One wave per chain: the world frame at every segment's x2, composed in double from the
-// first frame (the one the head segment used) and the segment totals.  Lane l handles
-// segment 64c + l of chunk c: an ordered wave scan of the totals, then the running frame of
-// the earlier chunks in front.
+// One wave per chain: the world frame at every segment's x2, composed in double from x2 of
+// the first frame (the one the head segment used) and the segment totals, the head's total
+// already carrying the first frame's rotation (forward_chain composes it into the scan); the
+// head's own frame is the first frame.  Lane l handles segment 64c + l of chunk c: an ordered
+// wave scan of the totals, then the running frame of the earlier chunks in front.
 template <typename T>
 __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
     const T* __restrict__ lengths, const T* __restrict__ angles, const T* __restrict__ p0,
@@ -90,9 +91,7 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
   const T* Lr = lengths + b * (points - 1);
   const T* Ar = angles + b * (points - 2);
   const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
-  Rigid<double> run;  // world frame at x2 of the chunk's first segment
-#pragma unroll
-  for (int i = 0; i < 9; ++i) run.m[i] = static_cast<double>(ff.frame[i]);
+  Rigid<double> run = rigid_identity<double>();  // (I, x2) o the totals of earlier chunks
   run.v[0] = static_cast<double>(ff.p2.x);
   run.v[1] = static_cast<double>(ff.p2.y);
   run.v[2] = static_cast<double>(ff.p2.z);
@@ -108,7 +107,11 @@ __global__ __launch_bounds__(kLongThreads) void long_forward_frames_kernel(
       for (int i = 0; i < 3; ++i) t.v[i] = tj[9 + i];
     }
     const Rigid<double> incl = wave_prefix(t);
-    const Rigid<double> f = compose(run, wave_shift_up(incl, lane));
+    Rigid<double> f = compose(run, wave_shift_up(incl, lane));
+    if (j == 0) {
+#pragma unroll
+      for (int i = 0; i < 9; ++i) f.m[i] = static_cast<double>(ff.frame[i]);
+    }
     if (j < segments) {
       double* fj = st + j * kLongStateDoubles + 12;
 #pragma unroll

@@ -310,9 +310,32 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       for (int i = 0; i < 3; ++i) last_q[9 + i] = q.v[i];
     }
   }
+  // The first frame's rotation F enters the scan once, composed into the total of the chain's
+  // first lane (and given to that lane as its exclusive prefix), so every lane's prefix comes
+  // out as its world rotation and translation relative to x2, and no lane applies F afterwards
+  // (36 VALU once per workgroup instead of once per wave).  Explicit fmas, so that every kernel
+  // instance rounds the positions alike.  A segment after the head has F = identity; the head
+  // segment's total then includes F, which long_forward_frames_kernel accounts for.
+  Rigid<R> lane_total = narrow_rigid<R>(q);
+  Rigid<R> first = rigid_identity<R>();
+  if (wave == 0 && (!Segmented || head)) {
+    const R* const Fr = ff.frame;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) first.m[i] = Fr[i];
+    if (lane == 0) {
+      const Rigid<R> t = lane_total;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+          lane_total.m[3 * r + c] = fma(Fr[3 * r + 2], t.m[6 + c], fma(Fr[3 * r + 1], t.m[3 + c], Fr[3 * r] * t.m[c]));
+        lane_total.v[r] = fma(Fr[3 * r + 2], t.v[2], fma(Fr[3 * r + 1], t.v[1], Fr[3 * r] * t.v[0]));
+      }
+    }
+  }
   // lane_carry's barrier also publishes base[] and retires every read of the staged step
   // rows, which the point row below overwrites.
-  const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
+  const Rigid<R> excl = lane_carry<R, W>(lane_total, wave_total, lane, wave, first);
   if constexpr (Segmented) {
     if (last_lane) {
       Rigid<double> qt;
@@ -323,19 +346,13 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       store_total(total, excl, qt);
     }
   }
-  R F[9];
-#pragma unroll
-  for (int i = 0; i < 9; ++i) F[i] = base[i];
   const V3<R> p2 = {base[9], base[10], base[11]};
 
-  // World transform at the lane start: (F, p2) o excl.
+  // World transform at the lane start: (F, p2) o excl, with F already inside excl.
   R gm[9];
 #pragma unroll
-  for (int r = 0; r < 3; ++r) {
-#pragma unroll
-    for (int c = 0; c < 3; ++c) gm[3 * r + c] = F[3 * r] * excl.m[c] + F[3 * r + 1] * excl.m[3 + c] + F[3 * r + 2] * excl.m[6 + c];
-  }
-  const V3<R> gv = p2 + rot_apply(F, V3<R>{excl.v[0], excl.v[1], excl.v[2]});
+  for (int i = 0; i < 9; ++i) gm[i] = excl.m[i];
+  const V3<R> gv = {p2.x + excl.v[0], p2.y + excl.v[1], p2.z + excl.v[2]};
 
   R xmax = R(0);
   // The fused loss's share of this thread; superposed sums about the stored x2 and the
