@@ -172,7 +172,10 @@ __global__ __launch_bounds__(64 * W) void torsion_forward_kernel(const T* __rest
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     if (s0 + i < steps) {
-      const V3<R> x = gv + rot_apply(gm, V3<R>{y[i][0], y[i][1], y[i][2]});
+      // gv as the addend of the first fma: three issues per coordinate, not four.
+      const V3<R> x = {fma(gm[2], y[i][2], fma(gm[1], y[i][1], fma(gm[0], y[i][0], gv.x))),
+                       fma(gm[5], y[i][2], fma(gm[4], y[i][1], fma(gm[3], y[i][0], gv.y))),
+                       fma(gm[8], y[i][2], fma(gm[7], y[i][1], fma(gm[6], y[i][0], gv.z)))};
       if constexpr (Loss) {
         const V3<R> xs = stored(x);
         if constexpr (LossKind == kLossSuperposed) {
