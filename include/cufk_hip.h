@@ -210,8 +210,10 @@ int cufk_reconstruct_bwd_anchored_noalloc(int dtype, const void* lengths, const 
  * same dtype, loss (B,).  No reference counterpart: the reference reconstructs
  * (block.cu:319-329) and leaves the loss to PyTorch, whose kernels read xyz and the target,
  * write and read back the loss terms and grad_xyz, and hand grad_xyz to its backward
- * (block.cu:331-365).  Here the forward writes xyz and chain_regular exactly as
- * cufk_reconstruct_fwd_flagged does, plus the loss reduced from the positions in registers;
+ * (block.cu:331-365).  Here the forward writes xyz and chain_regular as
+ * cufk_reconstruct_fwd_flagged does (bit for bit, except for batches of at least 4096 chains of
+ * at most 131 points, which that entry point packs several to a wave and this one does not:
+ * there they agree within float rounding), plus the loss reduced from the positions in registers;
  * the backward reads xyz and the target and forms grad_xyz = 2 grad_loss[b] (x - target) in
  * LDS, so grad_xyz never exists in memory.  The loss uses the positions as stored (rounded to
  * the dtype).  grad_loss (B,) may be NULL (all ones).  4 <= N <= 2051.
@@ -245,7 +247,7 @@ int cufk_reconstruct_loss_bwd_anchored(int dtype, const void* lengths, const voi
  * (lengths, angles, dihedrals, anchors) as stored (rounded to the dtype) and t = target (B, N, 3).
  * The optimal rotation comes from Horn's quaternion method, solved per chain in double inside the
  * forward; no reference counterpart (the reference leaves losses to PyTorch).  The forward
- * writes xyz and chain_regular as cufk_reconstruct_fwd_flagged does, loss (B,) and
+ * writes xyz and chain_regular as cufk_reconstruct_loss_fwd does, loss (B,) and
  * superposition (B x CUFK_SUPERPOSITION_DOUBLES doubles).  The backward takes them (same
  * loss_kind) with grad_loss (B,) or NULL (ones) and forms grad_xyz = c (x_i - R^T (t_i - tbar) -
  * xbar) per point inside the kernel, c = (2/N) grad_loss[b] (divided by 2 rmsd for the RMSD; 0

@@ -597,6 +597,103 @@ def test_regularity_flags(cufk, device, dtype):
     assert torch.equal(xyz, ref)
 
 
+def _abi_fused():
+    import ctypes
+
+    lib = _abi()
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.cufk_reconstruct_loss_fwd.argtypes = [ci] + [vp] * 10 + [i64, i64, vp]
+    lib.cufk_reconstruct_superposed_fwd.argtypes = [ci, ci] + [vp] * 11 + [i64, i64, vp]
+    lib.cufk_torsion_fwd.argtypes = [ci, vp, i64, vp, vp, i64, i64, vp]
+    lib.cufk_torsion_loss_fwd.argtypes = [ci, ci, vp, i64, vp, vp, vp, vp, vp, i64, i64, vp]
+    return lib
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("B,N", [(40, 300), (9, 2049), (4100, 64)])
+def test_fused_forwards_store_the_flagged_forwards_positions(device, dtype, B, N):
+    """The fused-loss forwards (squared distance, superposed) write xyz and the regularity flags
+    as cufk_reconstruct_fwd_flagged does: bit for bit where that entry point runs one chain per
+    workgroup, within float rounding where it packs short chains (at least 4096 chains of at most
+    131 points; the fused forwards never pack).  The shadow forward's xyz is the plain forward's
+    bit for bit wherever it keeps a float copy.  The full-size fused-loss tests hold the fused
+    gradients to the adjoint over the plain forward's positions, so they rely on this."""
+    lib = _abi_fused()
+    code = _CODES[dtype]
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    d = _inputs(B, N, seed=N + B, anchors=True, dtype=dtype)
+    L, A, D = (_dev(d[k], dtype, device) for k in ("lengths", "angles", "dihedrals"))
+    an = _anchors3(d, dtype, device)
+    xyz, reg = _flagged_forward(lib, L, A, D, an)
+    target = (xyz.double() + 0.3 * torch.randn(B, N, 3, device=device, dtype=torch.float64)).to(dtype)
+    packed = B >= 4096 and N - 3 <= 128
+    scale = max(1.0, float(xyz.double().abs().max()))
+    tol = {torch.float32: 2e-6, torch.float64: 1e-12, torch.bfloat16: 2.0**-7}[dtype] * scale
+
+    def same(got, got_reg, what):
+        if packed:
+            err = float((got.double() - xyz.double()).abs().max())
+            assert err <= tol, (what, err, tol)
+        else:
+            assert torch.equal(got, xyz), what
+        assert torch.equal(got_reg, reg), what
+
+    fused = [("squared distance", None)] + [(f"superposed kind {k}", k) for k in (1, 2)]
+    for what, kind in fused:
+        x2 = torch.empty_like(xyz)
+        r2 = torch.full((B,), 7, device=device, dtype=torch.uint8)
+        loss = torch.empty(B, device=device, dtype=dtype)
+        if kind is None:
+            rc = lib.cufk_reconstruct_loss_fwd(code, p(L), p(A), p(D), *(p(t) for t in an), p(target), p(x2), p(r2),
+                                               p(loss), B, N, st)
+        else:
+            rec = torch.empty(B, 24, device=device, dtype=torch.float64)
+            rc = lib.cufk_reconstruct_superposed_fwd(code, kind, p(L), p(A), p(D), *(p(t) for t in an), p(target),
+                                                     p(x2), p(r2), p(loss), p(rec), B, N, st)
+        assert rc == 0, what
+        same(x2, r2, what)
+    if dtype == torch.bfloat16 and lib.cufk_reconstruct_shadow_floats(B, N) > 0:
+        x3 = torch.empty_like(xyz)
+        pos = torch.empty(B, N, 3, device=device, dtype=torch.float32)
+        r3 = torch.full((B,), 7, device=device, dtype=torch.uint8)
+        assert lib.cufk_reconstruct_fwd_shadow(code, p(L), p(A), p(D), *(p(t) for t in an), p(x3), p(pos), p(r3),
+                                               B, N, st) == 0
+        assert torch.equal(x3, xyz)
+        # The float copy rounds to the stored output.
+        assert torch.equal(pos.to(dtype), xyz)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("N", [300, 771])
+def test_torsion_loss_forward_stores_the_torsion_forwards_positions(device, dtype, N):
+    """cufk_torsion_loss_fwd writes xyz bit for bit as cufk_torsion_fwd does (both kinds)."""
+    import ctypes
+
+    class Consts(ctypes.Structure):
+        _fields_ = [("length", ctypes.c_float * 3), ("sin", ctypes.c_double * 3), ("cos", ctypes.c_double * 3)]
+
+    lib = _abi_fused()
+    code = _CODES[dtype]
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    c = Consts((ctypes.c_float * 3)(*BOND_LENGTHS), (ctypes.c_double * 3)(*(math.sin(a) for a in BOND_ANGLES)),
+               (ctypes.c_double * 3)(*(math.cos(a) for a in BOND_ANGLES)))
+    B = 40
+    gen = torch.Generator(device=device).manual_seed(N)
+    raw = torch.randn(B, 2 * (N - 3), generator=gen, device=device).to(dtype)
+    xyz = torch.empty(B, N, 3, device=device, dtype=dtype)
+    assert lib.cufk_torsion_fwd(code, p(raw), raw.stride(0), ctypes.byref(c), p(xyz), B, N, st) == 0
+    target = (xyz.double() + 0.3 * torch.randn(B, N, 3, device=device, dtype=torch.float64, generator=gen)).to(dtype)
+    for kind in (0, 1):
+        x2 = torch.empty_like(xyz)
+        loss = torch.empty(B, device=device, dtype=dtype)
+        rec = torch.empty(B, 24, device=device, dtype=torch.float64)
+        assert lib.cufk_torsion_loss_fwd(code, kind, p(raw), raw.stride(0), ctypes.byref(c), p(target), p(x2), p(loss),
+                                         p(rec), B, N, st) == 0
+        assert torch.equal(x2, xyz), kind
+
+
 def test_far_chain_is_not_regular_in_fp32(cufk, device):
     lib = _abi()
     d = _inputs(2, 50, seed=22, anchors=True, dtype=torch.float32)
