@@ -182,3 +182,31 @@ def test_anchor_gradients_long_chains_fp32_and_gradcheck(cufk, device):
     assert torch.autograd.gradcheck(
         lambda p, f, n: cufk.reconstruct_long(L, A, D, p, f, n, segment_steps=4, anchor_grads=True), an, eps=1e-6,
         atol=1e-7, rtol=1e-6)
+
+
+@pytest.mark.parametrize("path", ["reconstruct", "loss", "long"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("B,N", [(3, 300), (5, 2051), (4133, 67)])
+def test_anchored_backward_keeps_the_plain_gradients(cufk, device, path, dtype, B, N):
+    """With anchor_grads=True the gradients of lengths, angles and dihedrals are those of the
+    same call without it, bit for bit: the same kernels run, with a pointer for the anchor sums
+    they then also write."""
+    d = _case(B, N, seed=B + N, dtype=dtype)
+    g = _dev(d["grad"], dtype, device)
+    target = _dev(d["grad"], dtype, device)  # any (B, N, 3) row will do for the loss
+
+    def grads(anchored):
+        L, A, D = (_dev(d[k], dtype, device, True) for k in ("lengths", "angles", "dihedrals"))
+        an = [_dev(d[k], dtype, device, anchored) for k in ("p0", "first_direction", "initial_normal")]
+        if path == "reconstruct":
+            out, w = cufk.reconstruct(L, A, D, *an, anchor_grads=anchored), g
+        elif path == "loss":
+            out, w = cufk.reconstruct_loss(L, A, D, target, *an, anchor_grads=anchored), None
+        else:
+            out, w = cufk.reconstruct_long(L, A, D, *an, segment_steps=96, anchor_grads=anchored), g
+        if w is None:
+            return torch.autograd.grad(out.sum(), (L, A, D))
+        return torch.autograd.grad(out, (L, A, D), w)
+
+    for a, b, name in zip(grads(True), grads(False), ("lengths", "angles", "dihedrals")):
+        assert torch.equal(a, b), (path, name)
