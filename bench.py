@@ -16,11 +16,15 @@ Order of work:
    The steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB at
    config 2), so no step finds its inputs in the 256 MB last-level cache.
 3. Forward only: K forward calls without autograd, timed the same way (``forward_atoms_per_s``).
-4. Kernel split: K back-to-back launches of the forward entry point the step uses (the flagged
-   forward, through the C ABI) under one event pair give ``kernels.forward_us``; the backward
-   is the step minus that, so the two add up to the step.  (An event pair around each launch
-   would add a few microseconds per launch on this part.)
-5. ``--abi-reps`` back-to-back launches of each C-ABI entry point the step uses (0 by default).
+4. Kernel split: the device durations of the step's own kernels from torch.profiler's kernel
+   trace over up to 50 more steps of the same kind: ``kernels.forward_us``, ``backward_us``,
+   ``other_us`` (torch's kernels, e.g. a loss reduction) per step, and ``step_gap_us``, the step
+   minus all three (the GPU idle between kernels: launch gaps, host time).
+5. Each C-ABI entry point alone: K (or ``--abi-reps``) back-to-back launches of the step's
+   forward entry point, then of its backward entry point over each set's saved forward output,
+   each under one event pair (``kernels.abi_forward_us``, ``abi_backward_us``).
+6. For reconstruct and torsion configs run eagerly, the same step replayed from one HIP graph
+   per input set (``kernels.graph_step_us``; ``--no-graph-too`` skips it).
 
 ``roofline`` is for the step, the metric's own quantity: (forward + backward algorithmic bytes)
 / ms_per_step against MI355X's 8 TB/s HBM peak.  Algorithmic bytes per chain: forward s(6N-6)
@@ -35,8 +39,11 @@ The CPU baseline is the reference algorithm on this host's cores: serial float64
 over the chains with torch's intra-op threads, the median of 3 runs over the config's batch (or
 a subset of it where one run would take longer than about 20 s), scaled to atoms/s.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--config c2|c1|c3|c4_bf16|c4_fp16|long|short|loss|rmsd|torsion_loss] [--graph]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config NAME] [--graph]
+
+NAME is one of CONFIGS below: c1, c2 (the default, BASELINE.json's headline), c3, c4_bf16,
+c4_fp16, the extensions long, short, loss, rmsd, torsion_loss, and c2_far / c2_mixed (C2 with
+chains that take the exact backward).
 
 With --graph each input set's step is captured once in a HIP graph (torch.cuda.graph) and the
 timed steps replay the graphs: the kernels are the same, the per-step Python, autograd-engine and
@@ -77,7 +84,15 @@ CONFIGS = {
     # compile_torsion(...).loss (the torsion path fused with a coordinate loss) at C3's shape,
     # against the torsion path followed by the loss in torch.
     "torsion_loss": ("torsion_loss", "float32", 8192, 771),
+    # C2 with chains the position-based backward does not take (the exact recompute runs for
+    # them inside the same backward launch): every chain placed about 50 nm from the origin
+    # (p0 = (50, 0, 0) nm, past 256 of the shortest 0.12 nm bonds), and one chain in four with
+    # a near-straight bond angle (2.7 rad: sin 0.43 < 0.5).
+    "c2_far": ("reconstruct", "float32", 4096, 2049),
+    "c2_mixed": ("reconstruct", "float32", 4096, 2049),
 }
+# What the exact-fallback configs change in the C2 draws (see synthetic()).
+IRREGULAR = {"c2_far": "far", "c2_mixed": "quarter"}
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
 DTYPE_CODES = {"float32": 0, "float64": 1, "float16": 2, "bfloat16": 3}
@@ -93,6 +108,19 @@ MEASURED_TRAFFIC = {
 }
 
 
+HEADLINE_METRIC = "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline"  # BASELINE.json's metric
+
+
+def metric_name(config):
+    """The metric a config's line measures: BASELINE.json's headline for c2, the same quantity
+    named with its own kind, shape and dtype for the others."""
+    if config == "c2":
+        return HEADLINE_METRIC
+    kind, dtype_name, B, N = CONFIGS[config]
+    short = {"float32": "fp32", "float64": "fp64", "float16": "fp16", "bfloat16": "bf16"}[dtype_name]
+    return f"{kind} fwd+bwd atoms/sec @ B={B} N={N} {short} ({config}); % of HBM roofline"
+
+
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -106,6 +134,10 @@ def parse_args():
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--graph", action="store_true",
                    help="capture each input set's step (forward + torch.autograd.grad) in a HIP graph and time replays")
+    p.add_argument("--no-kernel-trace", dest="kernel_trace", action="store_false",
+                   help="skip the torch.profiler pass that splits the step into its kernels (e.g. under rocprofv3)")
+    p.add_argument("--no-graph-too", dest="graph_too", action="store_false",
+                   help="skip timing the step replayed from HIP graphs beside the eager step")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=3, help="CPU baseline runs (the median is reported)")
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="rough cap on one CPU baseline run")
@@ -129,7 +161,10 @@ def copy_probe(mib):
     return 0
 
 
-def synthetic(B, N, seed, torch, device, dtype):
+def synthetic(B, N, seed, torch, device, dtype, irregular=None):
+    """Config 2 draws.  irregular="far" moves p0 to (50, 0, 0) nm, so every chain sits past
+    the fp32 position-based backward's extent test; "quarter" sets one bond angle of every
+    fourth chain (chains 0, 4, 8, ...) to 2.7 rad, past its angle test (sin 0.43 < 0.5)."""
     gen = torch.Generator().manual_seed(seed)
     L = (torch.randn(B, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
     A = torch.randn(B, N - 2, generator=gen, dtype=torch.float64) * 0.08 + 2.05
@@ -137,6 +172,10 @@ def synthetic(B, N, seed, torch, device, dtype):
     g = torch.randn(B, N, 3, generator=gen, dtype=torch.float64)
     p0 = torch.randn(3, generator=gen, dtype=torch.float64)
     q, _ = torch.linalg.qr(torch.randn(3, 3, generator=gen, dtype=torch.float64))
+    if irregular == "far":
+        p0 = torch.tensor([50.0, 0.0, 0.0], dtype=torch.float64)
+    elif irregular == "quarter":
+        A[::4, (N - 2) // 2] = 2.7
     cast = lambda t: t.to(device=device, dtype=dtype).contiguous()  # noqa: E731
     return cast(L), cast(A), cast(D), cast(g), cast(p0), cast(q[:, 0]), cast(q[:, 1])
 
@@ -155,6 +194,49 @@ def event_time_ms(torch, fn, reps):
     b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b) / reps
+
+
+def kernel_direction(name):
+    """Which half of a step a library kernel belongs to, from its name (None: not ours)."""
+    if "cufk_amd::" not in name:
+        return None
+    if "backward" in name or "anchor_gradients" in name:
+        return "backward"
+    if "forward" in name or "superpose_records" in name:
+        return "forward"
+    return None
+
+
+def in_step_kernel_times(torch, steps, nsets, n):
+    """Average device time per step of the step's forward kernels, backward kernels and any
+    other kernels (torch's own, e.g. a loss's reduction), and per kernel, from torch.profiler's
+    kernel trace over n steps; None if the profiler is unavailable."""
+    try:
+        from torch.profiler import ProfilerActivity, profile
+
+        for i in range(3):
+            steps[i % nsets]()
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for i in range(n):
+                steps[i % nsets]()
+            torch.cuda.synchronize()
+        sums = {"forward": 0.0, "backward": 0.0, "other": 0.0}
+        per_kernel = {}
+        for e in prof.events():
+            if e.device_type != torch.autograd.DeviceType.CUDA:
+                continue
+            t = float(e.device_time)
+            sums[kernel_direction(e.name) or "other"] += t
+            short = e.name.split("(")[0].replace("void ", "").replace("cufk_amd::", "")
+            per_kernel.setdefault(short, []).append(t)
+        if sums["forward"] == 0.0:
+            return None
+        return {"forward_us": sums["forward"] / n, "backward_us": sums["backward"] / n, "other_us": sums["other"] / n,
+                "per_kernel_us": {k: sum(v) / len(v) for k, v in sorted(per_kernel.items())}, "steps": n}
+    except Exception as exc:  # noqa: BLE001 - the split is a report, never a reason to lose the line
+        print(f"kernel split unavailable: {exc!r}", file=sys.stderr)
+        return None
 
 
 def coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device, chains=64):
@@ -434,7 +516,7 @@ def main():
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
         for k in range(nsets):
-            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype)
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype, IRREGULAR.get(args.config))
             L.requires_grad_(True)
             A.requires_grad_(True)
             D.requires_grad_(True)
@@ -599,22 +681,52 @@ def main():
         torch.cuda.synchronize()
     ms_forward_only = f_start.elapsed_time(f_end) / args.steps
 
-    # 4. Kernel split of the step: K launches of the step's own forward entry point (the flagged
-    # forward through the C ABI) back to back under one event pair, rotating over the same sets;
-    # the backward is the rest of the step.  Event pairs around single launches would not do:
-    # each event adds a few microseconds on this part.
-    st = ctypes.c_void_p(stream.cuda_stream)
-    for i in range(nsets):
-        fwds[i](st)  # also writes each set's regularity flags
-    seg_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.steps)
-    seg_bwd = ms_per_step - seg_fwd
+    # 4. Kernel split of the step: the device durations of the step's own kernels, read from
+    # torch.profiler's kernel trace over a pass of the same steps (same sets, same order):
+    # forward and backward kernels averaged per step, step_gap_us the step minus both.
+    split = in_step_kernel_times(torch, steps, nsets, min(args.steps, 50)) if args.kernel_trace else None
 
-    # 5. Optional: each C-ABI entry point alone, back to back, rotating over the same sets.
-    t_fwd = t_bwd = None
-    if args.abi_reps > 0:
-        t_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), args.abi_reps)
-        t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), args.abi_reps)
+    # 5. Each C-ABI entry point alone: K back-to-back launches of the step's forward entry point
+    # (the flagged forward) under one event pair, rotating over the same sets, then K launches of
+    # its backward entry point over each set's saved forward output.  Back to back, a launch
+    # never finds its input in the last-level cache the way the step's backward finds the
+    # forward's output there, and it pays the gap between launches; so these sit above the
+    # in-step durations at large configs.  (An event pair around each launch would add a few
+    # microseconds per launch on this part.)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    abi_reps = args.abi_reps if args.abi_reps > 0 else args.steps
+    for i in range(nsets):
+        fwds[i](st)  # each set's saved output (and regularity flags) for the backward
+    t_fwd = event_time_ms(torch, lambda i: fwds[i % nsets](st), abi_reps)
+    for i in range(nsets):
+        fwds[i](st)
+    t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), abi_reps)
     regular_frac = float(torch.stack(regular).float().mean()) if regular else None
+
+    # 6. The same step replayed from HIP graphs (eager runs only, reconstruct and torsion): one
+    # graph per input set, captured after warm-up on a side stream, replayed back to back.  With
+    # the per-step Python, autograd-engine and launch overhead gone it shows how much of the
+    # eager step is host time (all of the difference at small configs such as c1).
+    graph_ms = None
+    if not args.graph and kind in ("reconstruct", "torsion") and args.graph_too:
+        graphs = []
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for k in range(nsets):
+                for _ in range(3):
+                    steps[k]()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        for k in range(nsets):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                steps[k]()
+            graphs.append(graph)
+        for i in range(args.warmup):
+            graphs[i % nsets].replay()
+        graph_ms = event_time_ms(torch, lambda i: graphs[i % nsets].replay(), args.steps)
+        del graphs
 
     unfused_us = None
     if kind in ("loss", "rmsd", "torsion_loss"):  # the same step unfused (the loss in torch), same input sets
@@ -640,7 +752,7 @@ def main():
     frac = lambda nbytes, ms: None if ms is None else gbs(nbytes, ms) / HBM_PEAK_GBS  # noqa: E731
     traffic = MEASURED_TRAFFIC.get(args.config)
     result = {
-        "metric": "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline",
+        "metric": metric_name(args.config),
         "value": atoms / (ms_per_step * 1e-3),
         "unit": "atoms/s",
         "n_gpus": 1,
@@ -668,19 +780,26 @@ def main():
             "avg_step_us": ms_per_step * 1e3,
         },
         "kernels": {
-            "forward_us": us(seg_fwd),
-            "backward_us": us(seg_bwd),
-            "split": "forward: K back-to-back launches of the step's forward entry point; backward: the step minus "
-                     "that (so it also holds the gaps between launches)",
-            "forward_frac": frac(fwd_bytes, seg_fwd),
-            "backward_frac": frac(bwd_bytes, seg_bwd),
+            "forward_us": None if split is None else split["forward_us"],
+            "backward_us": None if split is None else split["backward_us"],
+            "other_us": None if split is None else split["other_us"],
+            "step_gap_us": None if split is None else ms_per_step * 1e3 - split["forward_us"] - split["backward_us"]
+            - split["other_us"],
+            "per_kernel_us": None if split is None else split["per_kernel_us"],
+            "split": "device durations of the step's kernels (torch.profiler kernel trace over "
+                     f"{None if split is None else split['steps']} steps of the timed kind, averaged per step): "
+                     "forward kernels, backward kernels, other (torch's) kernels; step_gap_us: the step minus all three",
+            "forward_frac": None if split is None else frac(fwd_bytes, split["forward_us"] * 1e-3),
+            "backward_frac": None if split is None else frac(bwd_bytes, split["backward_us"] * 1e-3),
             "forward_algorithmic_bytes": fwd_bytes,
             "backward_algorithmic_bytes": bwd_bytes,
             "forward_only_us": ms_forward_only * 1e3,
             "abi_forward_us": us(t_fwd),
             "abi_backward_us": us(t_bwd),
+            "abi_split": f"{abi_reps} back-to-back launches each of the forward and backward C-ABI entry points",
             "regular_chain_fraction": regular_frac,
             "unfused_step_us": unfused_us,
+            "graph_step_us": us(graph_ms),
         },
     }
     if precision is not None:

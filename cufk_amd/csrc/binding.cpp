@@ -139,6 +139,11 @@ int max_steps(const Tensor& ref, int direction) {
 
 void* current_stream(const Tensor& ref) { return c10::hip::getCurrentHIPStream(ref.get_device()).stream(); }
 
+// The version counter of an output kept for the backward.  An output made under
+// torch.inference_mode() has none (reading it raises), but no backward is ever recorded for
+// it either, so any value does.
+int64_t saved_version(const Tensor& t) { return t.is_inference() ? 0 : static_cast<int64_t>(t._version()); }
+
 void check_status(int status, const char* what) {
   TORCH_CHECK(status == CUFK_OK, what, " failed: ", cufk_error_string(status));
 }
@@ -187,7 +192,7 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     // it is untouched at backward time, regular chains use the position-based adjoint;
     // if the caller modified it in place, every chain takes the exact recompute.
     ctx->saved_data["xyz"] = xyz.detach();
-    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["xyz_version"] = saved_version(xyz);
     ctx->saved_data["regular"] = regular;
     return xyz;
   }
@@ -271,7 +276,7 @@ class AnchoredAutograd : public torch::autograd::Function<AnchoredAutograd> {
                  "cufk_reconstruct_fwd_flagged");
     ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
     ctx->saved_data["xyz"] = xyz.detach();
-    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["xyz_version"] = saved_version(xyz);
     ctx->saved_data["regular"] = regular;
     return xyz;
   }
@@ -511,7 +516,7 @@ class LongReconstructAutograd : public torch::autograd::Function<LongReconstruct
     // the caller modified it in place, the backward recomputes it.
     ctx->save_for_backward({lengths, angles, dihedrals, a.p0, a.first_direction, a.initial_normal});
     ctx->saved_data["xyz"] = xyz.detach();
-    ctx->saved_data["xyz_version"] = static_cast<int64_t>(xyz._version());
+    ctx->saved_data["xyz_version"] = saved_version(xyz);
     ctx->saved_data["state"] = state;
     ctx->saved_data["segment_steps"] = seg;
     return xyz;
@@ -579,6 +584,15 @@ Tensor apply_reconstruct_long(const Tensor& lengths, const Tensor& angles, const
 
 // ------------------------------------------------------------------ torsion
 
+// The raw-pair gradient keeps the input's strides (torsion.cu:401, empty_strided_like), unless
+// the input's rows overlap (a row stride shorter than the row, as an unfold or as_strided view
+// can give): gradient rows laid out that way would overlap too, so it is dense instead.
+Tensor pair_gradient_like(const Tensor& raw_pairs) {
+  if (raw_pairs.size(0) > 1 && raw_pairs.stride(0) < raw_pairs.size(1))
+    return torch::empty(raw_pairs.sizes(), raw_pairs.options());
+  return torch::empty_strided(raw_pairs.sizes(), raw_pairs.strides(), raw_pairs.options());
+}
+
 cufk_torsion_consts consts_from(const std::vector<double>& packed) {
   cufk_torsion_consts c;
   for (int i = 0; i < 3; ++i) {
@@ -618,7 +632,7 @@ class TorsionAutograd : public torch::autograd::Function<TorsionAutograd> {
     const auto list = ctx->saved_data["consts"].toDoubleList();
     const cufk_torsion_consts c = consts_from(std::vector<double>(list.begin(), list.end()));
     // extension_utils.cuh:162-164: the gradient keeps the raw tensor's strides.
-    Tensor grad = torch::empty_strided(raw_pairs.sizes(), raw_pairs.strides(), raw_pairs.options());
+    Tensor grad = pair_gradient_like(raw_pairs);
     check_status(cufk_torsion_bwd(dtype_code(raw_pairs), raw_pairs.data_ptr(), raw_pairs.stride(0), xyz.data_ptr(),
                                   grad_points.data_ptr(), grad.data_ptr(), grad.stride(0), &c, shape.batch, shape.points,
                                   current_stream(raw_pairs)),
@@ -675,7 +689,7 @@ class TorsionLossAutograd : public torch::autograd::Function<TorsionLossAutograd
     const double* rec = nullptr;
     if (kind != CUFK_LOSS_SQUARED_DISTANCE) rec = static_cast<const double*>(ctx->saved_data["record"].toTensor().data_ptr());
     // extension_utils.cuh:162-164: the gradient keeps the raw tensor's strides.
-    Tensor grad = torch::empty_strided(raw_pairs.sizes(), raw_pairs.strides(), raw_pairs.options());
+    Tensor grad = pair_gradient_like(raw_pairs);
     check_status(cufk_torsion_loss_bwd(dtype_code(raw_pairs), kind, raw_pairs.data_ptr(), raw_pairs.stride(0),
                                        xyz.data_ptr(), target.data_ptr(), rec, grad_loss.data_ptr(), grad.data_ptr(),
                                        grad.stride(0), &c, shape.batch, shape.points, current_stream(raw_pairs)),
@@ -715,7 +729,8 @@ std::vector<int64_t> validate_reconstruct(const Tensor& lengths, const Tensor& a
                                           bool device) {
   const Shape shape = check_geom(lengths, angles, dihedrals, device);
   checked_anchors(p0, first_direction, initial_normal, lengths, device);
-  check_max_local_transforms(shape.points - 3, cufk_max_steps(dtype_code(lengths), CUFK_FORWARD, 0), "reconstruct");
+  const int64_t cap = device ? max_steps(lengths, CUFK_FORWARD) : CUFK_MAX_STEPS;
+  check_max_local_transforms(shape.points - 3, cap, "reconstruct");
   return {shape.batch, shape.points};
 }
 
@@ -725,7 +740,8 @@ void validate_grad_points(const Tensor& grad_points, const Tensor& lengths, bool
 
 std::vector<int64_t> validate_torsion(const Tensor& raw_pairs, bool device) {
   const Shape shape = check_pairs(raw_pairs, device);
-  check_max_local_transforms(shape.points - 3, cufk_max_steps(dtype_code(raw_pairs), CUFK_FORWARD, 0), "torsion_pairs");
+  const int64_t cap = device ? max_steps(raw_pairs, CUFK_FORWARD) : CUFK_MAX_STEPS;
+  check_max_local_transforms(shape.points - 3, cap, "torsion_pairs");
   return {shape.batch, shape.points};
 }
 

@@ -6,8 +6,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstdint>
+#include <cstring>
 #include <mutex>
 
 #include "launch.h"
@@ -35,6 +37,15 @@ inline int check_long(int64_t batch, int64_t points, int64_t seg_steps) {
 }
 
 inline bool valid_dtype(int dtype) { return dtype >= CUFK_FLOAT32 && dtype <= CUFK_BFLOAT16; }
+
+// Raw-pair row strides: reading rows that overlap is harmless, but gradient rows that overlap
+// (a stride shorter than the row's 2(N-3) values, more than one chain) would have workgroups
+// writing each other's elements.
+inline int check_pair_strides(int64_t raw_stride, int64_t grad_raw_stride, int64_t batch, int64_t points) {
+  if (raw_stride < 0 || grad_raw_stride < 0) return CUFK_ERR_STRIDE;
+  if (batch > 1 && grad_raw_stride < 2 * (points - 3)) return CUFK_ERR_STRIDE;
+  return CUFK_OK;
+}
 
 template <typename Fn> int dispatch(int dtype, Fn&& fn) {
   switch (dtype) {
@@ -86,6 +97,25 @@ inline int scratch_on_current_device(double** out) {
   }
   *out = address[dev];
   return CUFK_OK;
+}
+
+// Whether `device` is a present HIP device of the one architecture this library carries code
+// for (gfx950).  Cached per device index: the torch binding asks on every call.
+bool device_supported(int device) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<signed char> known[kMaxDevices] = {};  // 0 unknown, 1 supported, -1 not
+  if (device < 0 || device >= kMaxDevices) return false;
+  const signed char k = known[device].load(std::memory_order_relaxed);
+  if (k != 0) return k > 0;
+  int count = 0;
+  bool ok = hipGetDeviceCount(&count) == hipSuccess && device < count;
+  if (ok) {
+    hipDeviceProp_t prop;
+    ok = hipGetDeviceProperties(&prop, device) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+         (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':');
+  }
+  known[device].store(ok ? 1 : -1, std::memory_order_relaxed);
+  return ok;
 }
 
 }  // namespace cufk_amd
@@ -244,7 +274,8 @@ int cufk_torsion_bwd(int dtype, const void* raw_pairs, int64_t raw_stride, const
   if (!valid_dtype(dtype)) return CUFK_ERR_DTYPE;
   const int rc = check_chain(batch, points);
   if (rc != CUFK_OK) return rc;
-  if (raw_stride < 0 || grad_raw_stride < 0) return CUFK_ERR_STRIDE;
+  const int sc = check_pair_strides(raw_stride, grad_raw_stride, batch, points);
+  if (sc != CUFK_OK) return sc;
   if (!consts) return CUFK_ERR_NULL;
   if (batch == 0) return CUFK_OK;
   if (!raw_pairs || !xyz || !grad_xyz || !grad_raw) return CUFK_ERR_NULL;
@@ -460,7 +491,8 @@ int cufk_torsion_loss_bwd(int dtype, int loss_kind, const void* raw_pairs, int64
   if (loss_kind < CUFK_LOSS_SQUARED_DISTANCE || loss_kind > CUFK_LOSS_RMSD) return CUFK_ERR_LOSS;
   const int rc = check_chain(batch, points);
   if (rc != CUFK_OK) return rc;
-  if (raw_stride < 0 || grad_raw_stride < 0) return CUFK_ERR_STRIDE;
+  const int sc = check_pair_strides(raw_stride, grad_raw_stride, batch, points);
+  if (sc != CUFK_OK) return sc;
   if (!consts) return CUFK_ERR_NULL;
   if (batch == 0) return CUFK_OK;
   const bool superposed = loss_kind != CUFK_LOSS_SQUARED_DISTANCE;
@@ -561,10 +593,10 @@ int cufk_reconstruct_long_bwd_anchored(int dtype, const void* lengths, const voi
 }
 
 int cufk_max_steps(int dtype, int direction, int device) {
-  (void)device;
   if (!valid_dtype(dtype)) return -CUFK_ERR_DTYPE;
-  if (direction != CUFK_FORWARD && direction != CUFK_BACKWARD) return -CUFK_ERR_DTYPE;
-  return kMaxSteps;
+  if (direction != CUFK_FORWARD && direction != CUFK_BACKWARD) return -CUFK_ERR_DIRECTION;
+  if (!cufk_amd::device_supported(device)) return -CUFK_ERR_DEVICE;
+  return CUFK_MAX_STEPS;
 }
 
 const char* cufk_error_string(int status) {
@@ -575,12 +607,13 @@ const char* cufk_error_string(int status) {
     case CUFK_ERR_SHAPE: return "shape exceeds int32 kernel limits";
     case CUFK_ERR_STEPS: return "too many local transforms";
     case CUFK_ERR_NULL: return "null pointer argument";
-    case CUFK_ERR_STRIDE: return "negative row stride";
+    case CUFK_ERR_STRIDE: return "negative row stride, or gradient row stride shorter than the row";
     case CUFK_ERR_LAUNCH: return "kernel launch failed";
     case CUFK_ERR_DEVICE: return "device query failed";
     case CUFK_ERR_SEGMENT: return "segment length must be in [1, 2048] local transforms";
     case CUFK_ERR_SCRATCH: return "batch exceeds the 65536 chains of the allocation-free entry point's static scratch";
     case CUFK_ERR_LOSS: return "unknown or unsupported loss kind";
+    case CUFK_ERR_DIRECTION: return "direction must be CUFK_FORWARD or CUFK_BACKWARD";
     default: return "unknown status";
   }
 }

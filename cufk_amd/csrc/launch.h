@@ -19,7 +19,7 @@
 
 namespace cufk_amd {
 
-constexpr int kMaxSteps = 2048;  // block.cu:88, torsion.cu:97 (512 threads x 4 items)
+constexpr int kMaxSteps = CUFK_MAX_STEPS;  // block.cu:88, torsion.cu:97 (512 threads x 4 items)
 
 // Long chains: per-(chain, segment) state and backward scratch, in doubles.
 constexpr int kLongStateDoubles = 24;

@@ -36,12 +36,18 @@ def _anchor(x: torch.Tensor | None, vals: tuple[float, float, float], ref: torch
     The reference builds it with a host-to-device copy on every call.  Here it is built once per
     device, dtype and value and reused: the kernels only read it and it never requires grad, so
     the values and gradients are the same, and a call with default anchors saves three small
-    copies (about 45 us of host time at C1's size)."""
+    copies (about 45 us of host time at C1's size).
+
+    The cached tensor is always made outside inference mode: a tensor made inside it is an
+    inference tensor, which ``save_for_backward`` refuses, so a first call under
+    ``torch.inference_mode()`` would otherwise break every later call that needs gradients."""
     if x is None:
         key = (ref.device, ref.dtype, vals)
         x = _DEFAULT_ANCHORS.get(key)
         if x is None:
-            x = _DEFAULT_ANCHORS.setdefault(key, torch.tensor(vals, device=ref.device, dtype=ref.dtype))
+            with torch.inference_mode(False):
+                made = torch.tensor(vals, device=ref.device, dtype=ref.dtype)
+            x = _DEFAULT_ANCHORS.setdefault(key, made)
     return x
 
 

@@ -38,12 +38,14 @@ enum cufk_status {
   CUFK_ERR_SHAPE = 3,       /* "shape exceeds int32 kernel limits" (extension_utils.cuh:120) */
   CUFK_ERR_STEPS = 4,       /* more local transforms than the step cap (extension_utils.cuh:128-130) */
   CUFK_ERR_NULL = 5,        /* a required pointer is NULL while B > 0 */
-  CUFK_ERR_STRIDE = 6,      /* raw-pair row stride shorter than the row */
+  CUFK_ERR_STRIDE = 6,      /* negative raw-pair row stride, or (B > 1) a raw-pair gradient row stride shorter
+                             * than the row, which would make gradient rows overlap */
   CUFK_ERR_LAUNCH = 7,      /* kernel launch failed (C10_CUDA_KERNEL_LAUNCH_CHECK, block.cu:327) */
   CUFK_ERR_DEVICE = 8,      /* device query failed */
   CUFK_ERR_SEGMENT = 9,     /* long-chain segment length outside [1, 2048] */
   CUFK_ERR_SCRATCH = 10,    /* batch larger than the static scratch of an allocation-free entry point */
-  CUFK_ERR_LOSS = 11        /* unknown or unsupported loss kind */
+  CUFK_ERR_LOSS = 11,       /* unknown or unsupported loss kind */
+  CUFK_ERR_DIRECTION = 12   /* cufk_max_steps: direction is neither CUFK_FORWARD nor CUFK_BACKWARD */
 };
 
 /* Fused loss kinds (cufk_torsion_loss_*, cufk_reconstruct_superposed_*). */
@@ -59,6 +61,10 @@ enum cufk_loss {
 
 /* Chains per call of cufk_reconstruct_bwd_anchored_noalloc (its static scratch: 6 doubles each). */
 #define CUFK_NOALLOC_MAX_CHAINS 65536
+
+/* The step cap (N-3) of every dtype and direction on the architecture the library is built
+ * for: what cufk_max_steps returns for a supported device (block.cu:88, torsion.cu:97). */
+#define CUFK_MAX_STEPS 2048
 
 /* Direction argument of cufk_max_steps. */
 enum cufk_direction { CUFK_FORWARD = 0, CUFK_BACKWARD = 1 };
@@ -327,7 +333,10 @@ int cufk_reconstruct_long_bwd_anchored(int dtype, const void* lengths, const voi
 
 /*
  * Largest step count (N-3) accepted for (dtype, direction) on `device`, or a negative
- * status.  Replaces kMaxSteps (block.cu:88, torsion.cu:97) and dynamic_shared_plan_limit
+ * status: -CUFK_ERR_DTYPE, -CUFK_ERR_DIRECTION, or -CUFK_ERR_DEVICE when `device` is not a
+ * present HIP device of the architecture the library is built for (gfx950).  Every kernel's
+ * LDS fits that architecture, so the cap is 2048 for each dtype and direction.  Replaces
+ * kMaxSteps (block.cu:88, torsion.cu:97) and dynamic_shared_plan_limit
  * (extension_utils.cuh:190-199).
  */
 int cufk_max_steps(int dtype, int direction, int device);

@@ -102,11 +102,22 @@ def test_status_strings(lib):
     assert lib.cufk_version() == b"0.1.0"
 
 
+ERR_DEVICE, ERR_DIRECTION = 8, 12
+
+
 def test_max_steps(lib):
-    for dtype in range(4):
-        assert lib.cufk_max_steps(dtype, 0, 0) == 2048
-        assert lib.cufk_max_steps(dtype, 1, 0) == 2048
+    # Argument checks come before the device query; no device index below 0 or past the
+    # present devices is supported (this host may have no GPU at all: then none is).
     assert lib.cufk_max_steps(9, 0, 0) == -ERR_DTYPE
+    assert lib.cufk_max_steps(0, 2, 0) == -ERR_DIRECTION
+    assert lib.cufk_max_steps(0, -1, 0) == -ERR_DIRECTION
+    for dtype in range(4):
+        for direction in range(2):
+            assert lib.cufk_max_steps(dtype, direction, -1) == -ERR_DEVICE
+            assert lib.cufk_max_steps(dtype, direction, 4096) == -ERR_DEVICE
+            assert lib.cufk_max_steps(dtype, direction, 0) in (2048, -ERR_DEVICE)
+    assert lib.cufk_error_string(ERR_DIRECTION) == b"direction must be CUFK_FORWARD or CUFK_BACKWARD"
+    assert lib.cufk_error_string(ERR_DEVICE) == b"device query failed"
 
 
 def test_reconstruct_status_paths(lib):
@@ -172,6 +183,15 @@ def test_torsion_status_paths(lib):
     assert f(0, p, 14, p, p, 0, 10, null) == OK
     b = lib.cufk_torsion_bwd
     assert b(0, p, 14, p, p, p, -3, p, 2, 10, null) == ERR_STRIDE
+    # Gradient rows (14 values at N = 10) must not overlap: a shorter row stride is refused
+    # for two chains or more; one chain has no second row to overlap (the stride check passes
+    # and the missing gradient pointer is what is refused).  Overlapping raw rows are only read.
+    assert b(0, p, 14, p, p, p, 13, p, 2, 10, null) == ERR_STRIDE
+    assert b(0, p, 14, p, p, p, 0, p, 2, 10, null) == ERR_STRIDE
+    assert b(0, p, 3, p, p, null, 14, p, 2, 10, null) == ERR_NULL
+    assert b(0, p, 14, p, p, null, 3, p, 1, 10, null) == ERR_NULL
+    assert b(0, p, 14, p, p, null, 0, p, 1, 10, null) == ERR_NULL
+    assert lib.cufk_error_string(ERR_STRIDE) == b"negative row stride, or gradient row stride shorter than the row"
     assert b(3, p, 14, p, p, p, 14, p, 2, 3, null) == ERR_POINTS
 
 
@@ -286,6 +306,8 @@ def test_fused_loss_status_paths(lib):
     #         dtype kind raw stride xyz tgt rec gl graw gstride consts
     assert tb(0, 1, p, 10, p, p, null, null, p, 10, p, 4, 8, null) == ERR_NULL
     assert tb(0, 0, p, 10, p, p, null, null, p, -2, p, 4, 8, null) == ERR_STRIDE
+    assert tb(0, 0, p, 10, p, p, null, null, p, 9, p, 4, 8, null) == ERR_STRIDE  # rows of 10 would overlap
+    assert tb(0, 0, p, 10, p, p, null, null, null, 9, p, 1, 8, null) == ERR_NULL  # one chain: stride accepted
     assert lib.cufk_error_string(ERR_LOSS) == b"unknown or unsupported loss kind"
 
 

@@ -82,3 +82,36 @@ def test_c2_trace_recomputes_the_stated_roofline_fraction():
     frac = 4 * B * (15 * N - 18) / (step_ns * 1e-9) / 8e12
     stated = float(re.search(r"\*\*(0\.\d+)\*\* of 8 TB/s", text).group(1))
     assert abs(frac - stated) <= 0.0015, (frac, stated)
+
+
+def test_metric_names_follow_the_config():
+    b = _bench()
+    assert b.metric_name("c2") == "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline"
+    assert b.metric_name("c2") == __import__("json").loads((ROOT / "BASELINE.json").read_text())["metric"]
+    assert b.metric_name("c1") == "reconstruct fwd+bwd atoms/sec @ B=1024 N=384 fp32 (c1); % of HBM roofline"
+    assert b.metric_name("c4_bf16") == "reconstruct fwd+bwd atoms/sec @ B=16384 N=1026 bf16 (c4_bf16); % of HBM roofline"
+    assert b.metric_name("c3").startswith("torsion fwd+bwd atoms/sec @ B=8192 N=771 fp32")
+    assert len({b.metric_name(c) for c in b.CONFIGS}) == len(b.CONFIGS)
+
+
+def test_exact_fallback_configs_break_the_position_tests():
+    """c2_far puts every chain past the fp32 extent test (max |x| <= 256 x shortest bond); c2_mixed
+    gives exactly every fourth chain an angle past the sine test (sin < 0.5), the rest pass it."""
+    import math
+
+    import torch
+
+    from oracle import cpu_torch as ct
+
+    b = _bench()
+    B, N = 64, 2049
+    L, A, D, g, p0, fd, n0 = b.synthetic(8, N, 2, torch, "cpu", torch.float64, "far")
+    assert p0.tolist() == [50.0, 0.0, 0.0]
+    x = ct.forward(L, A, D, p0, fd, n0)
+    assert (x.abs().amax(dim=(1, 2)) > 256 * L.amin(dim=1)).all()
+    L, A, D, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64, "quarter")
+    bad = (torch.sin(A) < 0.5).any(dim=1)
+    assert bad.tolist() == [i % 4 == 0 for i in range(B)]
+    assert math.isclose(float(torch.sin(torch.tensor(2.7))), 0.427, abs_tol=1e-3)
+    L2, A2, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64)
+    assert torch.equal(L, L2) and torch.equal(A[1::4], A2[1::4])

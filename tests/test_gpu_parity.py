@@ -387,6 +387,41 @@ def test_torsion_strided_rows_keep_grad_strides(cufk, device):
     del leaf
 
 
+def test_torsion_overlapping_rows_get_a_dense_gradient(cufk, device):
+    """Raw rows that overlap (row stride shorter than the row, as an as_strided or unfold view
+    gives) are read as they lie; their gradient cannot keep that layout (its rows would
+    overlap), so it comes back dense, each row the gradient of its own chain."""
+    rng = np.random.default_rng(6)
+    B, N = 5, 40
+    K = 2 * (N - 3)
+    flat = torch.as_tensor(rng.normal(size=K + 6 * (B - 1)), dtype=torch.float64, device=device)
+    raw = flat.as_strided((B, K), (6, 1))
+    assert raw.stride(0) < K
+    leaf = raw.detach().clone().requires_grad_(True)  # the same values, dense rows
+    f = cufk.compile_torsion(BOND_LENGTHS, BOND_ANGLES)
+    g = _dev(rng.normal(size=(B, N, 3)), torch.float64, device)
+    view = flat.clone().requires_grad_(True)
+    out = f(view.as_strided((B, K), (6, 1)))
+    (gv,) = torch.autograd.grad(out, (view,), g, retain_graph=True)
+    want_x = f(leaf)
+    (want_g,) = torch.autograd.grad(want_x, (leaf,), g)
+    assert torch.equal(out, want_x)
+    # Autograd sums the rows' gradients back into the flat storage they share.
+    summed = torch.zeros_like(flat)
+    for b in range(B):
+        summed[6 * b : 6 * b + K] += want_g[b]
+    assert torch.allclose(gv, summed, rtol=0, atol=1e-12)
+
+
+def test_max_steps_on_the_device(device):
+    from cufk_amd._native import _C
+
+    for dtype in range(4):
+        for direction in range(2):
+            assert _C.max_steps(dtype, direction, 0) == 2048
+    assert _C.max_steps(0, 0, torch.cuda.device_count()) == -8
+
+
 # ----------------------------------------------------------------- low precision (reported)
 
 
