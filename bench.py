@@ -16,14 +16,12 @@ Order of work:
    The steps rotate over ``--sets`` independent input batches (3 by default, about 1.2 GB at
    config 2), so no step finds its inputs in the 256 MB last-level cache.
 3. Forward only: K forward calls without autograd, timed the same way (``forward_atoms_per_s``).
-4. Kernel split: the device durations of the step's own kernels from torch.profiler's kernel
-   trace over up to 50 more steps of the same kind: ``kernels.forward_us``, ``backward_us``,
-   ``other_us`` (torch's kernels, e.g. a loss reduction) per step, and ``step_gap_us``, the step
-   minus all three (the GPU idle between kernels: launch gaps, host time).
-5. Each C-ABI entry point alone: K (or ``--abi-reps``) back-to-back launches of the step's
-   forward entry point, then of its backward entry point over each set's saved forward output,
-   each under one event pair (``kernels.abi_forward_us``, ``abi_backward_us``).
-6. For reconstruct and torsion configs run eagerly, the same step replayed from one HIP graph
+4. Kernel split: K (or ``--abi-reps``) back-to-back launches of the step's forward C-ABI entry
+   point, then of its backward entry point over each set's saved forward output, each under one
+   event pair: ``kernels.forward_us``, ``backward_us``, and ``step_gap_us`` = the step minus both.
+   ``--phases`` splits a rocprofv3 kernel trace of the same command into the kernels' in-step
+   and back-to-back durations.
+5. For reconstruct and torsion configs run eagerly, the same step replayed from one HIP graph
    per input set (``kernels.graph_step_us``; ``--no-graph-too`` skips it).
 
 ``roofline`` is for the step, the metric's own quantity: (forward + backward algorithmic bytes)
@@ -134,8 +132,9 @@ def parse_args():
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--graph", action="store_true",
                    help="capture each input set's step (forward + torch.autograd.grad) in a HIP graph and time replays")
-    p.add_argument("--no-kernel-trace", dest="kernel_trace", action="store_false",
-                   help="skip the torch.profiler pass that splits the step into its kernels (e.g. under rocprofv3)")
+    p.add_argument("--phases", metavar="KERNEL_TRACE_CSV",
+                   help="only split a rocprofv3 kernel trace of a bench run into its in-step and back-to-back "
+                        "phases (JSON) and exit; needs no GPU")
     p.add_argument("--no-graph-too", dest="graph_too", action="store_false",
                    help="skip timing the step replayed from HIP graphs beside the eager step")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -207,36 +206,37 @@ def kernel_direction(name):
     return None
 
 
-def in_step_kernel_times(torch, steps, nsets, n):
-    """Average device time per step of the step's forward kernels, backward kernels and any
-    other kernels (torch's own, e.g. a loss's reduction), and per kernel, from torch.profiler's
-    kernel trace over n steps; None if the profiler is unavailable."""
-    try:
-        from torch.profiler import ProfilerActivity, profile
+def trace_phases(path):
+    """Split a rocprofv3 kernel trace (``--kernel-trace --output-format csv``) of one bench run
+    into its phases by the order of our dispatches: a forward or backward kernel between two of
+    the other direction ran inside a step; one between two of its own direction ran back to back
+    (the C-ABI passes).  Returns, per phase, the dispatch count and the mean and median duration
+    of each direction, and the median gap from the previous dispatch's end (microseconds)."""
+    import csv
 
-        for i in range(3):
-            steps[i % nsets]()
-        torch.cuda.synchronize()
-        with profile(activities=[ProfilerActivity.CUDA]) as prof:
-            for i in range(n):
-                steps[i % nsets]()
-            torch.cuda.synchronize()
-        sums = {"forward": 0.0, "backward": 0.0, "other": 0.0}
-        per_kernel = {}
-        for e in prof.events():
-            if e.device_type != torch.autograd.DeviceType.CUDA:
-                continue
-            t = float(e.device_time)
-            sums[kernel_direction(e.name) or "other"] += t
-            short = e.name.split("(")[0].replace("void ", "").replace("cufk_amd::", "")
-            per_kernel.setdefault(short, []).append(t)
-        if sums["forward"] == 0.0:
-            return None
-        return {"forward_us": sums["forward"] / n, "backward_us": sums["backward"] / n, "other_us": sums["other"] / n,
-                "per_kernel_us": {k: sum(v) / len(v) for k, v in sorted(per_kernel.items())}, "steps": n}
-    except Exception as exc:  # noqa: BLE001 - the split is a report, never a reason to lose the line
-        print(f"kernel split unavailable: {exc!r}", file=sys.stderr)
-        return None
+    with open(path, newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    ours = [(kernel_direction(r["Kernel_Name"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in rows]
+    ours = [o for o in ours if o[0] is not None]
+    acc = {}
+    for prev, cur, nxt in zip(ours, ours[1:], ours[2:]):
+        if prev[0] != cur[0] and nxt[0] != cur[0]:
+            phase = "in_step"
+        elif prev[0] == cur[0] == nxt[0]:
+            phase = "back_to_back"
+        else:
+            continue
+        a = acc.setdefault(phase, {"forward": [], "backward": [], "gap": []})
+        a[cur[0]].append((cur[2] - cur[1]) / 1e3)
+        a["gap"].append((cur[1] - prev[2]) / 1e3)
+    med = lambda v: sorted(v)[len(v) // 2] if v else None  # noqa: E731
+    out = {}
+    for phase, a in acc.items():
+        out[phase] = {"gap_median_us": med(a["gap"])}
+        for d in ("forward", "backward"):
+            v = a[d]
+            out[phase][d] = {"n": len(v), "mean_us": sum(v) / len(v) if v else None, "median_us": med(v)}
+    return out
 
 
 def coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device, chains=64):
@@ -355,6 +355,9 @@ def main():
 
     if args.copy_probe:
         return copy_probe(args.copy_probe)
+    if args.phases:
+        print(json.dumps(trace_phases(args.phases)))
+        return 0
 
     import torch
 
@@ -681,18 +684,15 @@ def main():
         torch.cuda.synchronize()
     ms_forward_only = f_start.elapsed_time(f_end) / args.steps
 
-    # 4. Kernel split of the step: the device durations of the step's own kernels, read from
-    # torch.profiler's kernel trace over a pass of the same steps (same sets, same order):
-    # forward and backward kernels averaged per step, step_gap_us the step minus both.
-    split = in_step_kernel_times(torch, steps, nsets, min(args.steps, 50)) if args.kernel_trace else None
-
-    # 5. Each C-ABI entry point alone: K back-to-back launches of the step's forward entry point
-    # (the flagged forward) under one event pair, rotating over the same sets, then K launches of
-    # its backward entry point over each set's saved forward output.  Back to back, a launch
-    # never finds its input in the last-level cache the way the step's backward finds the
-    # forward's output there, and it pays the gap between launches; so these sit above the
-    # in-step durations at large configs.  (An event pair around each launch would add a few
-    # microseconds per launch on this part.)
+    # 4. Kernel split: K back-to-back launches of the step's forward entry point (the flagged
+    # forward, through the C ABI) under one event pair, rotating over the same sets, then K
+    # launches of its backward entry point over each set's saved forward output.  Inside the
+    # step the backward finds part of its forward's output in the 256 MB last-level cache and the
+    # next forward follows a backward whose stores bypass it; back to back over rotating sets
+    # neither holds, so at large configs these durations sit a few percent above the in-step
+    # ones and step_gap_us (the step minus both) goes negative.  rocprofv3's kernel trace of the
+    # same run gives both phases (``--phases``).  An event pair around each launch would add a few
+    # microseconds per launch on this part.
     st = ctypes.c_void_p(stream.cuda_stream)
     abi_reps = args.abi_reps if args.abi_reps > 0 else args.steps
     for i in range(nsets):
@@ -703,7 +703,7 @@ def main():
     t_bwd = event_time_ms(torch, lambda i: bwds[i % nsets](st), abi_reps)
     regular_frac = float(torch.stack(regular).float().mean()) if regular else None
 
-    # 6. The same step replayed from HIP graphs (eager runs only, reconstruct and torsion): one
+    # 5. The same step replayed from HIP graphs (eager runs only, reconstruct and torsion): one
     # graph per input set, captured after warm-up on a side stream, replayed back to back.  With
     # the per-step Python, autograd-engine and launch overhead gone it shows how much of the
     # eager step is host time (all of the difference at small configs such as c1).
@@ -780,23 +780,18 @@ def main():
             "avg_step_us": ms_per_step * 1e3,
         },
         "kernels": {
-            "forward_us": None if split is None else split["forward_us"],
-            "backward_us": None if split is None else split["backward_us"],
-            "other_us": None if split is None else split["other_us"],
-            "step_gap_us": None if split is None else ms_per_step * 1e3 - split["forward_us"] - split["backward_us"]
-            - split["other_us"],
-            "per_kernel_us": None if split is None else split["per_kernel_us"],
-            "split": "device durations of the step's kernels (torch.profiler kernel trace over "
-                     f"{None if split is None else split['steps']} steps of the timed kind, averaged per step): "
-                     "forward kernels, backward kernels, other (torch's) kernels; step_gap_us: the step minus all three",
-            "forward_frac": None if split is None else frac(fwd_bytes, split["forward_us"] * 1e-3),
-            "backward_frac": None if split is None else frac(bwd_bytes, split["backward_us"] * 1e-3),
+            "forward_us": us(t_fwd),
+            "backward_us": us(t_bwd),
+            "step_gap_us": us(ms_per_step - t_fwd - t_bwd),
+            "split": f"forward and backward: {abi_reps} back-to-back launches each of the step's forward and backward "
+                     "C-ABI entry points under one event pair (the backward over each set's saved forward output); "
+                     "step_gap_us: the step minus both (negative where the step's backward reads its forward's output "
+                     "from the last-level cache)",
+            "forward_frac": frac(fwd_bytes, t_fwd),
+            "backward_frac": frac(bwd_bytes, t_bwd),
             "forward_algorithmic_bytes": fwd_bytes,
             "backward_algorithmic_bytes": bwd_bytes,
             "forward_only_us": ms_forward_only * 1e3,
-            "abi_forward_us": us(t_fwd),
-            "abi_backward_us": us(t_bwd),
-            "abi_split": f"{abi_reps} back-to-back launches each of the forward and backward C-ABI entry points",
             "regular_chain_fraction": regular_frac,
             "unfused_step_us": unfused_us,
             "graph_step_us": us(graph_ms),

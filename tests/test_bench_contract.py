@@ -115,3 +115,22 @@ def test_exact_fallback_configs_break_the_position_tests():
     assert math.isclose(float(torch.sin(torch.tensor(2.7))), 0.427, abs_tol=1e-3)
     L2, A2, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64)
     assert torch.equal(L, L2) and torch.equal(A[1::4], A2[1::4])
+
+
+def test_trace_phases_split(tmp_path):
+    """--phases: a dispatch between two of the other direction is in a step, one between two of
+    its own direction is back to back; torch's kernels are not ours and are skipped."""
+    b = _bench()
+    head = "Kind,Kernel_Name,Start_Timestamp,End_Timestamp\n"
+    f, bw, other = "void cufk_amd::reconstruct_forward_kernel<float>(x)", "void cufk_amd::reconstruct_backward_saved_kernel<float>(x)", "void at::native::copy(x)"
+    seq = [(f, 0, 40), (bw, 40, 90), (other, 90, 95), (f, 100, 140), (bw, 140, 190), (f, 190, 230), (bw, 232, 282),
+           (f, 300, 345), (f, 345, 390), (f, 391, 436), (f, 436, 481)]
+    lines = "".join(f'K,"{n}",{a * 1000},{e * 1000}\n' for n, a, e in seq)
+    path = tmp_path / "trace.csv"
+    path.write_text(head + lines)
+    out = b.trace_phases(str(path))
+    assert out["in_step"]["forward"]["n"] == 2 and out["in_step"]["backward"]["n"] == 3
+    assert out["in_step"]["forward"]["mean_us"] == 40.0 and out["in_step"]["backward"]["mean_us"] == 50.0
+    assert out["back_to_back"]["forward"]["n"] == 2 and out["back_to_back"]["forward"]["mean_us"] == 45.0
+    assert out["back_to_back"]["backward"]["n"] == 0 and out["back_to_back"]["gap_median_us"] == 1.0
+    assert b.kernel_direction(other) is None and b.kernel_direction(f) == "forward"

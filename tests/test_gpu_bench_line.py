@@ -1,7 +1,6 @@
 """bench.py's JSON line on the GPU: a short run per config checks the fields the driver and the
-tables read (metric, value, roofline, the direct kernel split and its step gap, the
-graph-replayed step) and, for the exact-fallback configs, the regular-chain fraction their
-inputs are built to give."""
+tables read (metric, value, roofline, the kernel split and its step gap, the graph-replayed step)
+and, for the exact-fallback configs, the regular-chain fraction their inputs are built to give."""
 
 from __future__ import annotations
 
@@ -36,13 +35,9 @@ def test_bench_line_fields(device, config):
     assert r["metric"] == bench.metric_name(config) and r["n_gpus"] == 1 and r["value"] > 0
     assert r["roofline"]["bound"] == "hbm" and 0 < r["roofline"]["frac"] < 1
     assert k["forward_us"] > 0 and k["backward_us"] > 0 and k["graph_step_us"] > 0
-    assert k["abi_forward_us"] > 0 and k["abi_backward_us"] > 0
     step_us = r["ms_per_step"] * 1e3
-    gap = step_us - k["forward_us"] - k["backward_us"] - k["other_us"]
-    assert k["step_gap_us"] == pytest.approx(gap, abs=1e-6)
+    assert k["step_gap_us"] == pytest.approx(step_us - k["forward_us"] - k["backward_us"], abs=1e-6)
     assert k["forward_frac"] < 1 and k["backward_frac"] < 1
-    names = " ".join(k["per_kernel_us"])
-    assert ("torsion_forward_kernel" if config == "c3" else "reconstruct_forward_kernel") in names
 
 
 @pytest.mark.parametrize("config,fraction", [("c2_far", 0.0), ("c2_mixed", 0.75)])
