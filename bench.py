@@ -28,8 +28,10 @@ Order of work:
 / ms_per_step against MI355X's 8 TB/s HBM peak.  Algorithmic bytes per chain: forward s(6N-6)
 (read lengths, angles, dihedrals; write xyz), backward s(9N-12) (read the three parameter rows'
 worth and grad_xyz; write the three gradients).  ``traffic`` is what rocprofv3's FETCH_SIZE and
-WRITE_SIZE counters read for the two kernels, per step (MEASURED_TRAFFIC below, copied from the
-committed summaries under profiles/).  ``kernels`` splits the step: forward and backward
+WRITE_SIZE counters read for the step's kernels (MEASURED_TRAFFIC below, copied from the
+committed summary under profiles/).  ``roofline_valu`` is the VALU roofline of the step's
+forward launch: its VALU instructions (MEASURED_VALU) over its duration (pass 4) against the
+1024 SIMDs' issue rate.  ``kernels`` splits the step: forward and backward
 durations from pass 4 and each one's fraction of the HBM peak.
 
 The CPU baseline is the reference algorithm on this host's cores: serial float64 NeRF
@@ -90,20 +92,30 @@ CONFIGS = {
     "c2_mixed": ("reconstruct", "float32", 4096, 2049),
 }
 # What the exact-fallback configs change in the C2 draws (see synthetic()).
-IRREGULAR = {"c2_far": "far", "c2_mixed": "quarter"}
+IRREGULAR = {"c2_far": "far", "c2_mixed": "every:4"}
 BOND_LENGTHS = (0.14685231, 0.15365194, 0.13405086)
 BOND_ANGLES = (1.9676635, 2.062335, 2.164016)
 DTYPE_CODES = {"float32": 0, "float64": 1, "float16": 2, "bfloat16": 3}
 ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 
-# HBM bytes per step (forward + backward launch) from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
-# each counter scaled by what it reads for a plain copy of known size; the per-kernel figures are
-# in profiles/hbm_traffic_c2_c3_c4.md.  A config without an entry reports traffic as null.
+# HBM bytes per step (every kernel of the forward and backward launches) from rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE in the bench's own regime, each counter scaled by what it reads for a
+# plain copy of known size, and the wave64 VALU instructions (SQ_INSTS_VALU) of the forward and
+# backward launches: profiles/counters_and_traffic_bench_regime.md.  A config without an entry
+# reports traffic and roofline_valu as null.
 MEASURED_TRAFFIC = {
-    "c2": 203257551 + 307661823,  # forward (read 102397237, write 100860314) + backward (202647346 + 105014477)
-    "c3": 126591291 + 254078872,  # torsion forward (50569224 + 76022067) + backward (203743538 + 50335334)
-    "c4_bf16": 415663340 + 411567446,  # forward with the float copy (105390111 + 310273229) + backward (306882902 + 104684544)
+    "c1": 24443993, "c2": 510671882, "c2_far": 511403161, "c2_mixed": 510923397, "c3": 380690801,
+    "c4_bf16": 826503391, "long": 914221555, "loss": 613204076, "rmsd": 616319160, "torsion_loss": 459006601,
+    "short": 500205623,
 }
+MEASURED_VALU = {  # (forward, backward) per launch
+    "c1": (1849344, 1108992), "c2": (20807680, 13934592), "c2_far": (20807680, 49778688),
+    "c2_mixed": (20806656, 22895616), "c3": (10616832, 11608064), "c4_bf16": (51197952, 34648064),
+    "long": (22353856, 22759616), "loss": (22761472, 14774272), "rmsd": (36455424, 18484715),
+    "torsion_loss": (12034048, 12230656), "short": (27754496, 23560192),
+}
+# VALU issue peak: 1024 SIMDs (256 CUs x 4) at 2.4 GHz, one wave64 instruction per 4 cycles each.
+VALU_PEAK_PER_S = 1024 * 2.4e9 / 4
 
 
 HEADLINE_METRIC = "fwd+bwd atoms/sec @ B=4096 N=2049 fp32; % of HBM roofline"  # BASELINE.json's metric
@@ -132,6 +144,9 @@ def parse_args():
     p.add_argument("--sets", type=int, default=3, help="independent input batches the steps rotate over")
     p.add_argument("--graph", action="store_true",
                    help="capture each input set's step (forward + torch.autograd.grad) in a HIP graph and time replays")
+    p.add_argument("--irregular", metavar="PATTERN",
+                   help="reconstruct configs: chains the position-based backward refuses, as 'far' (p0 50 nm from "
+                        "the origin), 'every:K' (every K-th chain) or 'first:F' (the first fraction F of the chains)")
     p.add_argument("--phases", metavar="KERNEL_TRACE_CSV",
                    help="only split a rocprofv3 kernel trace of a bench run into its in-step and back-to-back "
                         "phases (JSON) and exit; needs no GPU")
@@ -162,8 +177,9 @@ def copy_probe(mib):
 
 def synthetic(B, N, seed, torch, device, dtype, irregular=None):
     """Config 2 draws.  irregular="far" moves p0 to (50, 0, 0) nm, so every chain sits past
-    the fp32 position-based backward's extent test; "quarter" sets one bond angle of every
-    fourth chain (chains 0, 4, 8, ...) to 2.7 rad, past its angle test (sin 0.43 < 0.5)."""
+    the fp32 position-based backward's extent test; "every:K" sets the middle bond angle of
+    every K-th chain (chains 0, K, 2K, ...) to 2.7 rad, past its angle test (sin 0.43 < 0.5);
+    "first:F" does the same to the first fraction F of the chains (one contiguous block)."""
     gen = torch.Generator().manual_seed(seed)
     L = (torch.randn(B, N - 1, generator=gen, dtype=torch.float64) * 0.01 + 0.145).clamp_(0.12, 0.17)
     A = torch.randn(B, N - 2, generator=gen, dtype=torch.float64) * 0.08 + 2.05
@@ -173,8 +189,12 @@ def synthetic(B, N, seed, torch, device, dtype, irregular=None):
     q, _ = torch.linalg.qr(torch.randn(3, 3, generator=gen, dtype=torch.float64))
     if irregular == "far":
         p0 = torch.tensor([50.0, 0.0, 0.0], dtype=torch.float64)
-    elif irregular == "quarter":
-        A[::4, (N - 2) // 2] = 2.7
+    elif irregular is not None and irregular.startswith("every:"):
+        A[:: int(irregular[6:]), (N - 2) // 2] = 2.7
+    elif irregular is not None and irregular.startswith("first:"):
+        A[: round(B * float(irregular[6:])), (N - 2) // 2] = 2.7
+    elif irregular is not None:
+        raise ValueError(f"unknown irregular pattern {irregular!r}")
     cast = lambda t: t.to(device=device, dtype=dtype).contiguous()  # noqa: E731
     return cast(L), cast(A), cast(D), cast(g), cast(p0), cast(q[:, 0]), cast(q[:, 1])
 
@@ -197,7 +217,7 @@ def event_time_ms(torch, fn, reps):
 
 def kernel_direction(name):
     """Which half of a step a library kernel belongs to, from its name (None: not ours)."""
-    if "cufk_amd::" not in name:
+    if "cufk_amd" not in name:  # demangled (cufk_amd::...) or mangled (..8cufk_amd..) names
         return None
     if "backward" in name or "anchor_gradients" in name:
         return "backward"
@@ -519,7 +539,8 @@ def main():
         fwd_bytes = s * B * (6 * N - 6)
         bwd_bytes = s * B * (9 * N - 12)
         for k in range(nsets):
-            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype, IRREGULAR.get(args.config))
+            L, A, D, g, p0, fd, n0 = synthetic(B, N, 2 + k, torch, device, dtype,
+                                               args.irregular or IRREGULAR.get(args.config))
             L.requires_grad_(True)
             A.requires_grad_(True)
             D.requires_grad_(True)
@@ -797,6 +818,21 @@ def main():
             "graph_step_us": us(graph_ms),
         },
     }
+    valu = MEASURED_VALU.get(args.config)
+    if valu is not None:
+        # The VALU roofline of the step's forward launch (VALU-bound: the reconstruct forwards
+        # issue VALU for most of their cycles), with the backward's fraction beside it.
+        result["roofline_valu"] = {
+            "bound": "valu",
+            "kernel": f"{kind} forward launch (kernels.forward_us)",
+            "achieved": valu[0] / (t_fwd * 1e-3) / 1e9,
+            "peak": VALU_PEAK_PER_S / 1e9,
+            "unit": "G wave64 VALU instructions/s",
+            "frac": valu[0] / (t_fwd * 1e-3) / VALU_PEAK_PER_S,
+            "instructions": valu[0],
+            "backward_instructions": valu[1],
+            "backward_frac": valu[1] / (t_bwd * 1e-3) / VALU_PEAK_PER_S,
+        }
     if precision is not None:
         result["precision"] = precision
     if not args.no_cpu_baseline:

@@ -35,41 +35,52 @@ def test_headline_config_is_the_baseline_metric():
     assert b.CONFIGS["c4_bf16"] == ("reconstruct", "bfloat16", 16384, 1026)
 
 
-def _traffic_rows():
-    text = (ROOT / "profiles" / "hbm_traffic_c2_c3_c4.md").read_text()
-    rows = {}
-    for m in re.finditer(r"^\| (c2|c3|c4_bf16) \| ([^|]+) \|[^|]+\|[^|]+\| ([\d,]+) \| ([\d,]+) \| ([\d,]+) \| ([\d,]+) = ",
-                         text, re.M):
-        cfg, kernel = m.group(1), m.group(2).strip()
-        read, write, total, algorithmic = (int(m.group(k).replace(",", "")) for k in (3, 4, 5, 6))
-        rows.setdefault(cfg, []).append((kernel, read, write, total, algorithmic))
-    per_step = {m.group(1): int(m.group(2).replace(",", ""))
-                for m in re.finditer(r"(c2|c3|c4_bf16) ([\d,]+) B", text)}
-    return rows, per_step
+PROFILE = ROOT / "profiles" / "counters_and_traffic_bench_regime.md"
 
 
-def test_measured_traffic_matches_the_committed_profile():
+def _int(x):
+    return int(x.replace(",", ""))
+
+
+def _profile_rows():
+    """Per-kernel rows (config, kernel, read, written, total, algorithmic, VALU per launch) and
+    per-step rows (config: traffic, algorithmic, forward VALU, backward VALU) of the summary."""
+    text = PROFILE.read_text()
+    kernels, steps = {}, {}
+    num = r"([\d,]+)"
+    for m in re.finditer(rf"^\| (\w+) \| `([^`]+)` \| [\d.]+ \| {num} \| {num} \| {num} \| {num} \| {num} \|", text, re.M):
+        kernels.setdefault(m.group(1), []).append((m.group(2), *(_int(m.group(k)) for k in range(3, 8))))
+    for m in re.finditer(rf"^\| (\w+) \| {num} \| {num} \| [\d.]+ \| {num} \| {num} \|$", text, re.M):
+        steps[m.group(1)] = tuple(_int(m.group(k)) for k in range(2, 6))
+    return kernels, steps
+
+
+def test_measured_traffic_and_valu_match_the_committed_profile():
     b = _bench()
-    rows, per_step = _traffic_rows()
-    assert set(rows) == set(b.MEASURED_TRAFFIC) == set(per_step)
-    for cfg, kernels in rows.items():
-        assert len(kernels) == 2, cfg  # forward and backward
-        for _, read, write, total, _ in kernels:
-            assert read + write == total
-        assert sum(k[3] for k in kernels) == b.MEASURED_TRAFFIC[cfg] == per_step[cfg], cfg
+    kernels, steps = _profile_rows()
+    assert set(kernels) == set(steps) == set(b.MEASURED_TRAFFIC) == set(b.MEASURED_VALU)
+    for cfg, rows in kernels.items():
+        for _, read, write, total, _, _ in rows:
+            assert read + write == total, cfg
+        assert sum(r[3] for r in rows) == steps[cfg][0] == b.MEASURED_TRAFFIC[cfg], cfg
+        bwd = sum(r[5] for r in rows if any(w in r[0] for w in ("backward", "sums", "carry")))
+        fwd = sum(r[5] for r in rows) - bwd
+        assert (fwd, bwd) == steps[cfg][2:] == b.MEASURED_VALU[cfg], cfg
 
 
 def test_profile_algorithmic_bytes_follow_the_formulas():
     """The summary's algorithmic column: forward s(6N-6) and backward s(9N-12) bytes per chain
-    for reconstruct, s(5N-6) and s(10N-12) for torsion (s the element size)."""
+    for reconstruct, s(5N-6) and s(10N-12) for torsion (s the element size); the per-step
+    total is their sum, as the bench's own roofline counts it."""
     b = _bench()
-    rows, _ = _traffic_rows()
+    kernels, steps = _profile_rows()
     size = {"float32": 4, "bfloat16": 2}
-    for cfg, kernels in rows.items():
+    for cfg in ("c1", "c2", "c2_far", "c2_mixed", "c3", "c4_bf16", "short"):
         kind, dtype, B, N = b.CONFIGS[cfg]
         s = size[dtype]
         fwd, bwd = ((5 * N - 6), (10 * N - 12)) if kind == "torsion" else ((6 * N - 6), (9 * N - 12))
-        assert [k[4] for k in kernels] == [s * B * fwd, s * B * bwd], cfg
+        assert [k[4] for k in kernels[cfg]] == [s * B * fwd, s * B * bwd], cfg
+        assert steps[cfg][1] == s * B * (fwd + bwd), cfg
 
 
 def test_c2_trace_recomputes_the_stated_roofline_fraction():
@@ -109,9 +120,12 @@ def test_exact_fallback_configs_break_the_position_tests():
     assert p0.tolist() == [50.0, 0.0, 0.0]
     x = ct.forward(L, A, D, p0, fd, n0)
     assert (x.abs().amax(dim=(1, 2)) > 256 * L.amin(dim=1)).all()
-    L, A, D, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64, "quarter")
+    L, A, D, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64, b.IRREGULAR["c2_mixed"])
     bad = (torch.sin(A) < 0.5).any(dim=1)
     assert bad.tolist() == [i % 4 == 0 for i in range(B)]
+    for pattern, want in (("every:16", [i % 16 == 0 for i in range(B)]), ("first:0.25", [i < 16 for i in range(B)])):
+        A3 = b.synthetic(B, N, 2, torch, "cpu", torch.float64, pattern)[1]
+        assert (torch.sin(A3) < 0.5).any(dim=1).tolist() == want, pattern
     assert math.isclose(float(torch.sin(torch.tensor(2.7))), 0.427, abs_tol=1e-3)
     L2, A2, *_ = b.synthetic(B, N, 2, torch, "cpu", torch.float64)
     assert torch.equal(L, L2) and torch.equal(A[1::4], A2[1::4])
