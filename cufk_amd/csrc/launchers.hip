@@ -224,11 +224,12 @@ int reconstruct_bwd_saved_typed(const T* L, const T* A, const T* D, const T* p0,
   if (use_packed_bwd(B, N - 3))
     return packed_bwd_typed<T, true>(L, A, D, p0, fd, n0, xyz, regular, g, gL, gA, gD, B, N, st, anchor);
   return with_scan_plan(B, N - 3, [&]<int W, int K>() {
-    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+    return launch_chunks(B, 2 * 64 * W, [&](int64_t off, unsigned n) {  // room for the front workgroups
+      const unsigned grid = n + static_cast<unsigned>(front_groups(n));
+      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad>), dim3(grid), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
                          regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
-                         anchor != nullptr ? anchor + off * 6 : nullptr);
+                         int64_t{n}, anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
 }
@@ -238,11 +239,12 @@ int shadow_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* f
                      const uint8_t* regular, const T* g, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
   if (!use_shadow(B, N - 3)) return reconstruct_bwd_recompute_typed<T>(L, A, D, p0, fd, n0, g, gL, gA, gD, B, N, st);
   return with_scan_plan(B, N - 3, [&]<int W, int K>() {
-    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad, float>), dim3(n), dim3(64 * W), 0, st,
+    return launch_chunks(B, 2 * 64 * W, [&](int64_t off, unsigned n) {  // room for the front workgroups
+      const unsigned grid = n + static_cast<unsigned>(front_groups(n));
+      hipLaunchKernelGGL((reconstruct_backward_saved_kernel<T, W, K, kScanPad, float>), dim3(grid), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, pos + off * N * 3,
                          regular + off, g + off * N * 3, gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
-                         nullptr);
+                         int64_t{n}, nullptr);
     });
   });
 }
@@ -328,11 +330,12 @@ int loss_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const T* fd,
                    const uint8_t* regular, const T* target, const T* grad_loss, T* gL, T* gA, T* gD, int64_t B, int N,
                    hipStream_t st, double* anchor) {
   return with_scan_plan(B, N - 3, [&]<int W, int K>() {
-    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad>), dim3(n), dim3(64 * W), 0, st,
+    return launch_chunks(B, 2 * 64 * W, [&](int64_t off, unsigned n) {  // room for the front workgroups
+      const unsigned grid = FastPath<T>::kEnabled ? n + static_cast<unsigned>(front_groups(n)) : n;
+      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad>), dim3(grid), dim3(64 * W), 0, st,
                          L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
                          regular + off, target + off * N * 3, grad_loss != nullptr ? grad_loss + off : nullptr,
-                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N, nullptr, 0,
+                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N, int64_t{n}, nullptr, 0,
                          anchor != nullptr ? anchor + off * 6 : nullptr);
     });
   });
@@ -358,12 +361,13 @@ int superposed_bwd_typed(const T* L, const T* A, const T* D, const T* p0, const 
                          const uint8_t* regular, const T* target, const double* record, const T* grad_loss,
                          int squared, T* gL, T* gA, T* gD, int64_t B, int N, hipStream_t st) {
   return with_scan_plan(B, N - 3, [&]<int W, int K>() {
-    return launch_chunks(B, 64 * W, [&](int64_t off, unsigned n) {
-      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad, kLossSuperposed>), dim3(n), dim3(64 * W),
-                         0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0, xyz + off * N * 3,
-                         regular + off, target + off * N * 3, grad_loss != nullptr ? grad_loss + off : nullptr,
-                         gL + off * (N - 1), gA + off * (N - 2), gD + off * (N - 3), N,
-                         record + off * kSuperposeRecord, squared);
+    return launch_chunks(B, 2 * 64 * W, [&](int64_t off, unsigned n) {  // room for the front workgroups
+      const unsigned grid = FastPath<T>::kEnabled ? n + static_cast<unsigned>(front_groups(n)) : n;
+      hipLaunchKernelGGL((reconstruct_loss_backward_kernel<T, W, K, kScanPad, kLossSuperposed>), dim3(grid),
+                         dim3(64 * W), 0, st, L + off * (N - 1), A + off * (N - 2), D + off * (N - 3), p0, fd, n0,
+                         xyz + off * N * 3, regular + off, target + off * N * 3,
+                         grad_loss != nullptr ? grad_loss + off : nullptr, gL + off * (N - 1), gA + off * (N - 2),
+                         gD + off * (N - 3), N, int64_t{n}, record + off * kSuperposeRecord, squared);
     });
   });
 }

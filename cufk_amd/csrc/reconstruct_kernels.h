@@ -954,6 +954,61 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
   }
 }
 
+// ============================================================================ refused chains first
+
+// A chain the position-based adjoint refuses (regular flag 0) runs the exact path, which takes
+// about twice as long as a position-based chain.  Spread through the grid, the ones dispatched
+// last would set the kernel's end (at C2's shape, one refused chain in 64 took the backward from
+// 58 to 81 us, one in 16 to 97 us).  So the grids of the backwards that choose per chain start
+// with kFrontRanks front workgroups per group of kFrontGroup consecutive chains: front workgroup
+// r of a group takes the group's r-th refused chain, if any, and further on that chain's own
+// workgroup does nothing.  Up to kFrontRanks refused chains in every kFrontGroup thus start at
+// the head of the grid, and every chain is still processed by exactly one workgroup.
+//
+// Workgroups go to the eight XCDs round-robin by index, so two orders keep the exact work spread
+// over them: the front region is rank-major (every group's rank-0 workgroup, then rank 1, ...),
+// so the busy ones form a prefix whatever the number of refused chains per group; and group g
+// counts its chains from position 4g mod 16 (cyclically), so the chains whose own workgroups
+// skip do not always sit at the same positions, i.e. on the same XCDs.
+//
+// Measured at C2's shape (step, one box, interleaved): every chain regular 94.8-95.2 us for one,
+// two or four ranks alike; one refused chain in 4: 138.5, 112.6, 114.9 us for 1, 2, 4 ranks
+// (146 us before); one in 8: 106.6, 105.1, 106.2 us; every chain refused: 143.7, 148.1, 155.0 us
+// (148 us before), the skipping workgroups briefly holding LDS that exact ones could use.
+constexpr int kFrontGroup = 16;
+constexpr int kFrontRanks = 2;
+
+__host__ __device__ constexpr int64_t chain_groups(int64_t batch) { return (batch + kFrontGroup - 1) / kFrontGroup; }
+__host__ __device__ constexpr int64_t front_groups(int64_t batch) { return chain_groups(batch) * kFrontRanks; }
+
+// Group g's refused chains as a kFrontGroup-bit mask in its counting order: bit q for the chain
+// at position (q + 4g) mod kFrontGroup (chains at or past batch never refused).  Each wave loads
+// the group's flags itself, so the mask is uniform over the workgroup without LDS.
+__device__ __forceinline__ unsigned refused_mask(const uint8_t* __restrict__ regular, int64_t g, int64_t batch) {
+  const int lane = threadIdx.x & 63;
+  const int64_t chain = g * kFrontGroup + ((lane + 4 * g) & (kFrontGroup - 1));
+  return static_cast<unsigned>(__ballot(lane < kFrontGroup && chain < batch && regular[chain] == 0));
+}
+
+// The chain this backward workgroup takes (the grid is front_groups(batch) + batch
+// workgroups), or -1 for none.
+__device__ __forceinline__ int64_t backward_row(const uint8_t* __restrict__ regular, int64_t batch) {
+  const int64_t groups = chain_groups(batch);
+  const int64_t wg = blockIdx.x;
+  if (wg < groups * kFrontRanks) {
+    const int64_t g = wg % groups;
+    unsigned mask = refused_mask(regular, g, batch);
+    for (int r = static_cast<int>(wg / groups); r > 0 && mask != 0; --r) mask &= mask - 1;  // drop r lowest
+    return mask == 0 ? -1 : g * kFrontGroup + ((__builtin_ctz(mask) + 4 * g) & (kFrontGroup - 1));
+  }
+  const int64_t row = wg - groups * kFrontRanks;
+  if (regular[row] != 0) return row;
+  const int64_t g = row / kFrontGroup;
+  const int q = static_cast<int>((row - g * kFrontGroup - 4 * g) & (kFrontGroup - 1));  // counting position
+  return __builtin_popcount(refused_mask(regular, g, batch) & ((1u << q) - 1)) < kFrontRanks ? -1 : row;
+}
+
+
 // Backward without a saved output, one workgroup per chain.
 template <typename T, int W, int K, int Pad>
 __global__ __launch_bounds__(64 * W) void reconstruct_backward_recompute_kernel(
@@ -989,7 +1044,7 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const P* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ grad_xyz,
     T* __restrict__ grad_lengths, T* __restrict__ grad_angles, T* __restrict__ grad_dihedrals, int points,
-    double* __restrict__ anchor = nullptr) {
+    int64_t batch, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   constexpr int kA = 3 * Lay::kStepRow > Lay::kPointRow ? 3 * Lay::kStepRow : Lay::kPointRow;
@@ -998,7 +1053,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_backward_saved_kernel(
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
   __shared__ int wide_vote[W];
-  const int64_t row = blockIdx.x;
+  const int64_t row = backward_row(regular, batch);  // uniform over the workgroup
+  if (row < 0) return;
   double* const an = anchor != nullptr ? anchor + row * 6 : nullptr;
   T* gLr = grad_lengths + row * (points - 1);
   T* gAr = grad_angles + row * (points - 2);
@@ -1130,8 +1186,8 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
     const T* __restrict__ p0, const T* __restrict__ first_direction, const T* __restrict__ initial_normal,
     const T* __restrict__ xyz, const uint8_t* __restrict__ regular, const T* __restrict__ target,
     const T* __restrict__ grad_loss, T* __restrict__ grad_lengths, T* __restrict__ grad_angles,
-    T* __restrict__ grad_dihedrals, int points, const double* __restrict__ record = nullptr, int squared = 0,
-    double* __restrict__ anchor = nullptr) {
+    T* __restrict__ grad_dihedrals, int points, int64_t batch, const double* __restrict__ record = nullptr,
+    int squared = 0, double* __restrict__ anchor = nullptr) {
   using R = compute_t<T>;
   using Lay = Layout<W, K, Pad>;
   using Res = std::conditional_t<LossKind == kLossSuperposed, SuperposedResidual<R>, SquaredResidual<R>>;
@@ -1141,7 +1197,10 @@ __global__ __launch_bounds__(64 * W) void reconstruct_loss_backward_kernel(
   __shared__ R wave_total[W][12];
   __shared__ R wave_sum[W][6];
   __shared__ int wide_vote[W];
-  const int64_t row = blockIdx.x;
+  // Refused chains first (backward_row) where the position path exists; every half-type chain
+  // takes the exact path, in grid order.
+  const int64_t row = FastPath<T>::kEnabled ? backward_row(regular, batch) : static_cast<int64_t>(blockIdx.x);
+  if (row < 0) return;
   const int tid = threadIdx.x;
   {
     R* const dst[2] = {region_a, region_b};
