@@ -73,6 +73,10 @@ namespace cufk_amd {
 // 12.5 us; B=2048, N=700: 30.1 against 33.2 us.
 constexpr int kScanPad = 1;
 constexpr int64_t kLatencyWaves = 4096;
+//
+// Every plan gives each of its waves some of the chain's steps (a wave past the chain would still
+// run the lane scan, lane_scan_chain): where four waves of four or eight steps would leave the
+// last one idle (513-768 and 1025-1536 steps), the chain takes three.
 template <typename Fn> int with_scan_plan(int64_t groups, int steps, Fn&& fn) {
   if (steps <= 256) return fn.template operator()<1, 4>();
   if (steps <= 512) {
@@ -80,9 +84,13 @@ template <typename Fn> int with_scan_plan(int64_t groups, int steps, Fn&& fn) {
     return fn.template operator()<1, 8>();
   }
   if (steps <= 1024) {
-    if (2 * groups <= kLatencyWaves) return fn.template operator()<4, 4>();
+    if (2 * groups <= kLatencyWaves) {
+      if (steps <= 768) return fn.template operator()<3, 4>();
+      return fn.template operator()<4, 4>();
+    }
     return fn.template operator()<2, 8>();
   }
+  if (steps <= 1536) return fn.template operator()<3, 8>();
   return fn.template operator()<4, 8>();
 }
 

@@ -162,21 +162,22 @@ __device__ __forceinline__ void pad_lane_tail(R* Ls, R* As, R* Ds, int count) {
   }
 }
 
-// lane_scan over a whole chain: the hot instance unguarded (waves past the chain skip it;
-// lanes past it scan garbage that reaches no stored point and reset their flags), the
-// library-sin/cos instance guarded and one region per item (unguarded or unscheduled it needs
-// more registers than the hot one).
+// lane_scan over a whole chain: the hot instance unguarded (lanes past the chain scan garbage
+// that reaches no stored point and reset their flags), the library-sin/cos instance guarded and
+// one region per item (unguarded or unscheduled it needs more registers than the hot one).  No
+// wave skips the scan: every plan (with_scan_plan) gives each of its waves some of the chain's
+// steps, and a skip would cost every wave the registers' defaults for the waves that take it
+// (36 VALU per wave at C2).  q needs no starting value: each lane's first item sets it
+// (step_first), and lanes past the chain feed only later lanes, which store nothing either.
 template <typename T, int K, bool Table, typename Fast = FastPath<T>>
 __device__ __forceinline__ void lane_scan_chain(const compute_t<T>* Ls, const compute_t<T>* As,
-                                                const compute_t<T>* Ds, int count, bool wave_has_steps, bool wide,
+                                                const compute_t<T>* Ds, int count, bool wide,
                                                 const SinCosEntry* table, Rigid<double>& q, compute_t<T> (&y)[K][3],
                                                 bool& ok, compute_t<T>& lmin) {
-  if (wave_has_steps) {  // uniform per wave
-    if (wide)
-      lane_scan<T, K, true, true, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
-    else
-      lane_scan<T, K, false, false, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
-  }
+  if (wide)  // uniform per workgroup
+    lane_scan<T, K, true, true, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
+  else
+    lane_scan<T, K, false, false, Table, Fast>(Ls, As, Ds, count, table, q, y, ok, lmin);
   if (count <= 0) {
     ok = true;
     lmin = compute_t<T>(1.0e30);
@@ -257,7 +258,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
   // reaches them, so only y stays in registers.  Segments run it guarded: their last lane's
   // total transform is stored.  Measured at C2 (5 waves per SIMD), the table beats
   // sin_cos_wide (56.5 against 58.2 us).
-  Rigid<double> q = rigid_identity<double>();
+  Rigid<double> q;  // set by each lane's first step (step_first, lane_scan_chain)
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
@@ -274,8 +275,7 @@ __device__ __forceinline__ void forward_chain(const T* __restrict__ Lr, const T*
       else
         lane_scan<T, K, false, true, kTable>(Ls, As, Ds, count, sc_table, q, y, ok, lmin);
     } else {
-      lane_scan_chain<T, K, kTable, Fast>(Ls, As, Ds, count, wave * 64 * K < steps, wide, sc_table, q, y, ok,
-                                                lmin);
+      lane_scan_chain<T, K, kTable, Fast>(Ls, As, Ds, count, wide, sc_table, q, y, ok, lmin);
     }
   }
 
@@ -883,12 +883,12 @@ __device__ __forceinline__ void recompute_chain(const T* __restrict__ Lr, const 
   const FirstFrame<R> ff = first_frame<T>(widen(Lr[0]), widen(Lr[1]), widen(Ar[0]), p0, first_direction, initial_normal);
   wide = block_any<W>(wide, wide_vote, lane, wave);
 
-  Rigid<double> q = rigid_identity<double>();
+  Rigid<double> q;  // set by each lane's first step (lane_scan_chain)
   R y[K][3];
   bool ok = true;
   R lmin = R(1.0e30);
   lane_scan_chain<T, K, false, Fast>(pstage + b0, pstage + Lay::kStepRow + b0, pstage + 2 * Lay::kStepRow + b0,
-                                           count, wave * 64 * K < steps, wide, nullptr, q, y, ok, lmin);
+                                           count, wide, nullptr, q, y, ok, lmin);
   const Rigid<R> excl = lane_carry<R, W>(narrow_rigid<R>(q), wave_total, lane, wave);
 
   // World frame at the lane start, origin at x2.

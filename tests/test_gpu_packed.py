@@ -230,10 +230,11 @@ def test_packed_unaligned_storage(lib, device, dtype):
 
 # ----------------------------------------------------------------- plans chosen by batch and length
 #
-# One chain per workgroup for 257..1024 steps takes two plans, picked by the grid's size: small
-# grids (at most 4096 waves under the eight-item plan) take twice the waves at four items per
-# lane, larger grids eight items per lane.  Each (batch, length) below sits on one side of that
-# line, at a plan edge.
+# One chain per workgroup for 257..1024 steps takes two kinds of plan, picked by the grid's size:
+# small grids (at most 4096 waves under the eight-item plan) take twice the waves at four items
+# per lane, larger grids eight items per lane.  No plan leaves a wave without steps, so 513..768
+# steps take three waves of four and 1025..1536 three waves of eight.  Each (batch, length) below
+# sits on one side of one of those lines, at a plan edge.
 
 
 _PLAN_CASES = {}
@@ -252,7 +253,8 @@ def _plan_case(B, N):
 
 @pytest.mark.parametrize("recompute", [False, True])
 @pytest.mark.parametrize("B,N", [(1024, 260), (1024, 384), (1024, 515), (4097, 260), (4097, 515),
-                                 (1024, 516), (1024, 700), (2048, 1027), (2049, 516), (2049, 1027)])
+                                 (1024, 516), (1024, 700), (1024, 771), (1024, 772), (2048, 1027), (2049, 516),
+                                 (2049, 1027), (512, 1028), (512, 1539), (512, 1540)])
 def test_plans_by_batch_fp64(lib, device, B, N, recompute):
     """float64 forward within 1e-12 and gradients within 1e-10 of the oracle on every chain."""
     d, ref, ref_g = _plan_case(B, N)
@@ -263,7 +265,7 @@ def test_plans_by_batch_fp64(lib, device, B, N, recompute):
         assert np.abs(got.cpu().numpy() - want).max() <= 1e-10 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("B,N", [(1024, 384), (4097, 384), (1024, 1027), (2049, 1027)])
+@pytest.mark.parametrize("B,N", [(1024, 384), (4097, 384), (1024, 700), (1024, 1027), (2049, 1027), (512, 1200)])
 def test_plans_by_batch_fp32(cufk, device, B, N):
     """float32 through the autograd path: 1e-5 nm RMS and 1e-4 nm max forward, gradients 5e-5
     relative (normwise per chain)."""
