@@ -3,7 +3,9 @@ cufk_reconstruct_bwd_anchored with a caller-allocated workspace, through the C A
 
 Both run the same kernels on the same inputs, so every output is bit-identical.  Two calls in a
 row, the second on a smaller batch, show that the static scratch keeps no state a call depends
-on; both backward kinds (saved output and recompute) and float64/float32 are covered.
+on; both backward kinds (saved output and recompute) and float64/float32 are covered.  The entry
+point is also captured in a HIP graph and replayed, and warm calls are checked to leave the
+device's free memory unchanged.
 """
 
 from __future__ import annotations
@@ -98,3 +100,57 @@ def test_noalloc_rejects_batches_beyond_the_scratch(lib, device):
     assert rc == ERR_SCRATCH
     rc = lib.cufk_reconstruct_bwd_anchored_noalloc(0, *vp, MAX_CHAINS, 3, None)
     assert rc == 2  # point_count must be >= 4, checked first
+
+
+def test_noalloc_captured_in_a_graph_and_allocation_free(lib, device):
+    """The entry point is for callers that cannot allocate, graph capture first among them.
+    Captured in a HIP graph and replayed three times, with an eager call on other inputs (which
+    overwrites the shared scratch) and a synchronisation between replays, every replay equals
+    the eager call bit for bit.  Warm calls on fixed buffers leave the device's free memory as
+    it was."""
+    B, N, dtype = 2000, 300, torch.float32
+    p = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+
+    def buffers(seed):
+        t = _case(B, N, seed, dtype, device)
+        xyz = torch.empty(B, N, 3, dtype=dtype, device=device)
+        reg = torch.empty(B, dtype=torch.uint8, device=device)
+        an = [p(t[k]) for k in ("p0", "first_direction", "initial_normal")]
+        st = torch.cuda.current_stream().cuda_stream
+        assert lib.cufk_reconstruct_fwd_flagged(0, p(t["lengths"]), p(t["angles"]), p(t["dihedrals"]), *an, p(xyz),
+                                                p(reg), B, N, st) == 0
+        outs = [torch.empty_like(t[k]) for k in ("lengths", "angles", "dihedrals")]
+        outs += [torch.empty(3, dtype=dtype, device=device) for _ in range(3)]
+
+        def call():
+            s = torch.cuda.current_stream().cuda_stream  # the capture stream while capturing
+            rc = lib.cufk_reconstruct_bwd_anchored_noalloc(0, p(t["lengths"]), p(t["angles"]), p(t["dihedrals"]), *an,
+                                                           p(xyz), p(reg), p(t["grad"]), *map(p, outs), B, N, s)
+            assert rc == 0
+
+        return call, outs
+
+    call, outs = buffers(11)
+    other, _ = buffers(12)
+    call()
+    torch.cuda.synchronize()
+    want = [o_.clone() for o_ in outs]
+
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        for o_ in outs:
+            o_.fill_(float("nan"))
+        other()  # eager call on other inputs: the scratch now holds their sums
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, want):
+            assert torch.equal(a, b)
