@@ -23,6 +23,9 @@ Order of work:
    and back-to-back durations.
 5. For reconstruct and torsion configs run eagerly, the same step replayed from one HIP graph
    per input set (``kernels.graph_step_us``; ``--no-graph-too`` skips it).
+6. For c1 (or any reconstruct config with ``--host-breakdown``), the host time of the eager
+   step's pieces (``host``): the public forward, ``_C.apply`` alone, the backward alone, the
+   autograd engine's own hand-off for a one-op graph, the two C-ABI calls, the whole step.
 
 ``roofline`` is for the step, the metric's own quantity: (forward + backward algorithmic bytes)
 / ms_per_step against MI355X's 8 TB/s HBM peak.  Algorithmic bytes per chain: forward s(6N-6)
@@ -150,6 +153,8 @@ def parse_args():
     p.add_argument("--phases", metavar="KERNEL_TRACE_CSV",
                    help="only split a rocprofv3 kernel trace of a bench run into its in-step and back-to-back "
                         "phases (JSON) and exit; needs no GPU")
+    p.add_argument("--host-breakdown", action="store_true",
+                   help="reconstruct configs: time the host side of an eager step by piece (always on for c1)")
     p.add_argument("--no-graph-too", dest="graph_too", action="store_false",
                    help="skip timing the step replayed from HIP graphs beside the eager step")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -256,6 +261,43 @@ def trace_phases(path):
         for d in ("forward", "backward"):
             v = a[d]
             out[phase][d] = {"n": len(v), "mean_us": sum(v) / len(v) if v else None, "median_us": med(v)}
+    return out
+
+
+def host_breakdown(torch, cufk_amd, L, A, D, g, an, abi_pair, reps=1000):
+    """Host time per call (microseconds, no synchronisation inside the loop: at small configs
+    the host, not the GPU, bounds these) of the pieces of one eager step: the public forward
+    (Python wrapper and _C.apply, recording the backward), _C.apply alone, the backward alone
+    (torch.autograd.grad on a retained graph: the autograd engine plus the binding's backward),
+    the same engine hand-off for a one-op graph (L * 1.0), the step's two C-ABI calls through
+    ctypes, and the whole step."""
+    import time
+
+    from cufk_amd._native import _C
+
+    def per_call(fn):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) / reps * 1e6
+
+    x = cufk_amd.reconstruct(L, A, D, *an)
+    y = L * 1.0
+    gy = torch.ones_like(y)
+    out = {
+        "forward_call_us": per_call(lambda: cufk_amd.reconstruct(L, A, D, *an)),
+        "apply_us": per_call(lambda: _C.apply(L, A, D, *an)),
+        "backward_call_us": per_call(lambda: torch.autograd.grad(x, (L, A, D), g, retain_graph=True)),
+        "engine_one_op_backward_us": per_call(lambda: torch.autograd.grad(y, (L,), gy, retain_graph=True)),
+        "abi_pair_ctypes_us": per_call(abi_pair),
+        "step_us": per_call(lambda: torch.autograd.grad(cufk_amd.reconstruct(L, A, D, *an), (L, A, D), g)),
+    }
+    out["reps"] = reps
     return out
 
 
@@ -395,7 +437,7 @@ def main():
     i64 = ctypes.c_int64
 
     # One entry per input set: the autograd step and the two C-ABI calls it makes.
-    steps, fwds, bwds, regular, fonly = [], [], [], [], []
+    steps, fwds, bwds, regular, fonly, steps_inputs = [], [], [], [], [], []
     if kind == "long":
         # Algorithmic bytes as for reconstruct; the segment joins (placement, segment sums)
         # are extra traffic the roofline fraction is charged with.
@@ -584,6 +626,7 @@ def main():
             steps.append(step)
             fwds.append(fwd)
             bwds.append(bwd)
+            steps_inputs.append((L, A, D, g, p0, fd, n0))
             regular.append(flags)
             fonly.append(lambda L=L, A=A, D=D, p0=p0, fd=fd, n0=n0: cufk_amd.reconstruct(L, A, D, p0, fd, n0))
     else:
@@ -765,6 +808,11 @@ def main():
     precision = None
     if kind == "reconstruct":
         precision = coordinate_error_by_position(torch, cufk_amd, B, N, dtype, device)
+    host = None
+    if kind == "reconstruct" and (args.host_breakdown or args.config == "c1"):
+        L0, A0, D0, *_ = steps_inputs[0]
+        host = host_breakdown(torch, cufk_amd, L0, A0, D0, steps_inputs[0][3], steps_inputs[0][4:],
+                              lambda: (fwds[0](st), bwds[0](st)))
 
     atoms = B * N
     step_bytes = fwd_bytes + bwd_bytes
@@ -835,6 +883,8 @@ def main():
         }
     if precision is not None:
         result["precision"] = precision
+    if host is not None:
+        result["host"] = host
     if not args.no_cpu_baseline:
         v, chains, walls, threads = cpu_baseline(torch, kind, B, N, args.cpu_runs, args.cpu_seconds)
         result["cpu_baseline"] = {

@@ -124,6 +124,11 @@ Anchors checked_anchors(const Tensor& p0, const Tensor& fd, const Tensor& n0, co
   return {p0.contiguous(), fd.contiguous(), n0.contiguous()};
 }
 
+// The shape of a batch saved by a forward that validated it (check_geom).  Backwards take their
+// saved tensors as they are: they cannot change shape, dtype or device after the forward (the
+// reference checks them again, block.cu:422-428; only the incoming gradient is new here).
+Shape saved_shape(const Tensor& lengths) { return {lengths.size(0), lengths.size(1) + 1}; }
+
 // torsion.cu:413-417.
 Shape check_pairs(const Tensor& raw_pairs, bool device) {
   check_cuda_float_row_contiguous(raw_pairs, "raw_pairs", device);
@@ -205,8 +210,8 @@ class ReconstructAutograd : public torch::autograd::Function<ReconstructAutograd
     const Tensor& dihedrals = saved[2];
     Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_points, lengths, "grad_points", true);
-    const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true);
+    const Shape shape = saved_shape(lengths);
+    const Anchors a{saved[3], saved[4], saved[5]};
     const c10::DeviceGuard guard(lengths.device());
     const int64_t steps = shape.points - 3;
     const int64_t limit = max_steps(lengths, CUFK_BACKWARD);
@@ -289,8 +294,8 @@ class AnchoredAutograd : public torch::autograd::Function<AnchoredAutograd> {
     const Tensor& dihedrals = saved[2];
     Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_points, lengths, "grad_points", true);
-    const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true, true);
+    const Shape shape = saved_shape(lengths);
+    const Anchors a{saved[3], saved[4], saved[5]};
     const c10::DeviceGuard guard(lengths.device());
     Tensor grad_lengths = torch::empty_like(lengths);
     Tensor grad_angles = torch::empty_like(angles);
@@ -358,9 +363,9 @@ class LossAutograd : public torch::autograd::Function<LossAutograd> {
     const Tensor& angles = saved[1];
     const Tensor& dihedrals = saved[2];
     const Tensor& target = saved[3];
-    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Shape shape = saved_shape(lengths);
     const bool anchored = ctx->saved_data["anchored"].toBool();
-    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true, anchored);
+    const Anchors a{saved[4], saved[5], saved[6]};
     Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_loss, lengths, "grad_loss", true);
     const c10::DeviceGuard guard(lengths.device());
@@ -444,8 +449,8 @@ class SuperposedAutograd : public torch::autograd::Function<SuperposedAutograd> 
     const Tensor& angles = saved[1];
     const Tensor& dihedrals = saved[2];
     const Tensor& target = saved[3];
-    const Shape shape = check_geom(lengths, angles, dihedrals, true);
-    const Anchors a = checked_anchors(saved[4], saved[5], saved[6], lengths, true);
+    const Shape shape = saved_shape(lengths);
+    const Anchors a{saved[4], saved[5], saved[6]};
     Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_loss, lengths, "grad_loss", true);
     const c10::DeviceGuard guard(lengths.device());
@@ -530,9 +535,9 @@ class LongReconstructAutograd : public torch::autograd::Function<LongReconstruct
     const Tensor& dihedrals = saved[2];
     Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_points, lengths, "grad_points", true);
-    const Shape shape = check_geom(lengths, angles, dihedrals, true);
+    const Shape shape = saved_shape(lengths);
     const bool anchored = ctx->saved_data["anchored"].toBool();
-    const Anchors a = checked_anchors(saved[3], saved[4], saved[5], lengths, true, anchored);
+    const Anchors a{saved[3], saved[4], saved[5]};
     const c10::DeviceGuard guard(lengths.device());
     const int64_t seg = ctx->saved_data["segment_steps"].toInt();
     Tensor xyz = ctx->saved_data["xyz"].toTensor();
@@ -626,7 +631,7 @@ class TorsionAutograd : public torch::autograd::Function<TorsionAutograd> {
     const Tensor& xyz = saved[1];
     Tensor grad_points = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_points, raw_pairs, "grad_points", true);
-    const Shape shape = check_pairs(raw_pairs, true);
+    const Shape shape = Shape{raw_pairs.size(0), raw_pairs.size(1) / 2 + 3};
     const c10::DeviceGuard guard(raw_pairs.device());
     check_max_local_transforms(shape.points - 3, max_steps(raw_pairs, CUFK_FORWARD), "torsion_pairs");
     const auto list = ctx->saved_data["consts"].toDoubleList();
@@ -680,7 +685,7 @@ class TorsionLossAutograd : public torch::autograd::Function<TorsionLossAutograd
     const Tensor& target = saved[1];
     Tensor grad_loss = grad_outputs[0].is_contiguous() ? grad_outputs[0] : grad_outputs[0].contiguous();
     check_like(grad_loss, raw_pairs, "grad_loss", true);
-    const Shape shape = check_pairs(raw_pairs, true);
+    const Shape shape = Shape{raw_pairs.size(0), raw_pairs.size(1) / 2 + 3};
     const c10::DeviceGuard guard(raw_pairs.device());
     const auto list = ctx->saved_data["consts"].toDoubleList();
     const cufk_torsion_consts c = consts_from(std::vector<double>(list.begin(), list.end()));

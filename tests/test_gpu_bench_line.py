@@ -38,6 +38,9 @@ def test_bench_line_fields(device, config):
     step_us = r["ms_per_step"] * 1e3
     assert k["step_gap_us"] == pytest.approx(step_us - k["forward_us"] - k["backward_us"], abs=1e-6)
     assert k["forward_frac"] < 1 and k["backward_frac"] < 1
+    if config == "c1":
+        h = r["host"]
+        assert 0 < h["apply_us"] <= h["forward_call_us"] and h["backward_call_us"] > 0 and h["step_us"] > 0
     v = r["roofline_valu"]
     assert v["bound"] == "valu" and 0 < v["frac"] < 1 and 0 < v["backward_frac"] < 1
     assert v["achieved"] == pytest.approx(v["instructions"] / (k["forward_us"] * 1e-6) / 1e9)
