@@ -454,35 +454,50 @@ def test_low_precision_reported(cufk, device, dtype, N):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_low_precision_unaligned_storage(dtype, device):
-    """Rows whose storage starts 2 bytes past a 16-byte boundary (a view one element into a
-    buffer), through the C ABI: forward and exact backward equal those of the same values in
-    a fresh, aligned buffer, bit for bit."""
+@pytest.mark.parametrize("N", [301, 1100])
+@pytest.mark.parametrize("shift", range(1, 8))
+def test_low_precision_unaligned_storage(dtype, N, shift, device):
+    """float16/bfloat16 rows move in 8- or 4-element windows at the rows' own 2-byte alignment.
+    Every input and output here is a view `shift` elements into a buffer (storage 2*shift bytes
+    past a 16-byte boundary), through the C ABI: the forward, the exact backward and the shadow
+    forward and backward equal those of the same values in fresh, aligned buffers, bit for bit.
+    N = 301 runs 4-step lanes (4-element windows), N = 1100 8-step lanes (8-element windows);
+    both leave rows that end past their last whole window."""
     lib = _abi()
-    B, N = 5, 301
-    d = _inputs(B, N, seed=41, anchors=True, dtype=dtype)
+    B = 5
+    d = _inputs(B, N, seed=41 + shift, anchors=True, dtype=dtype)
     an = _anchors3(d, dtype, device)
+    aligned = lambda t, s: t  # noqa: E731
 
-    def shifted(x):
-        t = torch.as_tensor(x, dtype=dtype)
-        buf = torch.zeros(t.numel() + 8, dtype=dtype, device=device)
-        v = buf[1 : 1 + t.numel()].view(t.shape)
-        v.copy_(t.to(device))
-        assert v.data_ptr() % 16 == 2
+    def shifted(t, s):
+        buf = torch.full((t.numel() + 8,), float("nan"), dtype=t.dtype, device=device)
+        v = buf[s : s + t.numel()].view(t.shape)
+        v.copy_(t)
+        assert v.data_ptr() % 16 == (s * t.element_size()) % 16
         return v
 
     outs = []
-    for make in (lambda x: _dev(x, dtype, device), shifted):
-        L, A, D, g = (make(d[k]) for k in ("lengths", "angles", "dihedrals", "grad"))
-        xyz = torch.empty(B, N, 3, dtype=dtype, device=device)
-        gL, gA, gD = (torch.empty_like(t) for t in (L, A, D))
+    for make in (aligned, shifted):
+        L, A, D, g = (make(_dev(d[k], dtype, device), shift) for k in ("lengths", "angles", "dihedrals", "grad"))
+        blank = lambda t: make(torch.full_like(t, float("nan")), shift)  # noqa: E731
+        xyz, xyz2 = blank(g), blank(g)
+        gL, gA, gD, sL, sA, sD = (blank(t) for t in (L, A, D, L, A, D))
+        pos = torch.empty(B, N, 3, dtype=torch.float32, device=device)
+        reg = torch.empty(B, dtype=torch.uint8, device=device)
         p = lambda t: t.data_ptr()  # noqa: E731
         code, st = _CODES[dtype], torch.cuda.current_stream().cuda_stream
         assert lib.cufk_reconstruct_fwd(code, p(L), p(A), p(D), *map(p, an), p(xyz), B, N, st) == 0
         assert lib.cufk_reconstruct_bwd(code, p(L), p(A), p(D), *map(p, an), p(g), p(gL), p(gA), p(gD), B, N, st) == 0
+        assert lib.cufk_reconstruct_fwd_shadow(code, p(L), p(A), p(D), *map(p, an), p(xyz2), p(pos), p(reg), B, N,
+                                               st) == 0
+        assert lib.cufk_reconstruct_bwd_shadow(code, p(L), p(A), p(D), *map(p, an), p(pos), p(reg), p(g), p(sL), p(sA),
+                                               p(sD), B, N, st) == 0
         torch.cuda.synchronize()
-        outs.append((xyz.clone(), gL.clone(), gA.clone(), gD.clone()))
+        outs.append([t.clone() for t in (xyz, gL, gA, gD, xyz2, pos, reg, sL, sA, sD)])
+    assert torch.equal(outs[0][0], outs[0][4])  # the shadow forward's xyz is the plain forward's
+    assert bool(outs[0][6].all())  # every chain here takes the position-based backward
     for a, b in zip(*outs):
+        assert not a.is_floating_point() or torch.isfinite(a).all()
         assert torch.equal(a, b)
 
 
