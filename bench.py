@@ -107,14 +107,14 @@ ELEM_BYTES = {"float32": 4, "float64": 8, "float16": 2, "bfloat16": 2}
 # backward launches: profiles/counters_and_traffic_bench_regime.md.  A config without an entry
 # reports traffic and roofline_valu as null.
 MEASURED_TRAFFIC = {
-    "c1": 24443993, "c2": 510671882, "c2_far": 511403161, "c2_mixed": 510923397, "c3": 380690801,
-    "c4_bf16": 826503391, "long": 914221555, "loss": 613204076, "rmsd": 616319160, "torsion_loss": 459006601,
-    "short": 500205623,
+    "c1": 24429892, "c2": 510976820, "c2_far": 511569622, "c2_mixed": 511340596, "c3": 380682861,
+    "c4_bf16": 827142795, "long": 914240077, "loss": 613084106, "rmsd": 616138701, "torsion_loss": 458950537,
+    "short": 500206727,
 }
 MEASURED_VALU = {  # (forward, backward) per launch
-    "c1": (1849344, 1108992), "c2": (20807680, 13934592), "c2_far": (20807680, 49778688),
-    "c2_mixed": (20806656, 22895616), "c3": (10616832, 11608064), "c4_bf16": (51197952, 34648064),
-    "long": (22353856, 22759616), "loss": (22761472, 14774272), "rmsd": (36455424, 18484715),
+    "c1": (1796096, 1122816), "c2": (20185088, 14049280), "c2_far": (20185088, 49795072),
+    "c2_mixed": (20184064, 22985728), "c3": (10616832, 11608064), "c4_bf16": (42958848, 30072832),
+    "long": (22353856, 22759616), "loss": (22122496, 14872576), "rmsd": (36209664, 18583002),
     "torsion_loss": (12034048, 12230656), "short": (27754496, 23560192),
 }
 # VALU issue peak: 1024 SIMDs (256 CUs x 4) at 2.4 GHz, one wave64 instruction per 4 cycles each.
