@@ -714,6 +714,46 @@ def test_fused_forwards_store_the_flagged_forwards_positions(device, dtype, B, N
         assert torch.equal(pos.to(dtype), xyz)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [300, 1100])
+@pytest.mark.parametrize("shift", [0, 1, 3, 6])
+def test_torsion_low_precision_is_the_rounded_float32_forward(device, dtype, N, shift):
+    """The float16/bfloat16 torsion forward computes in float from the widened pairs, so its
+    output is the float32 forward's on the same values, rounded once, bit for bit.  Pairs and
+    output here are views `shift` elements into their buffers: the point rows (12-step lanes)
+    move in 4-element windows at the rows' own 2-byte alignment, the pairs element by element.
+    N = 300 runs one wave per chain, N = 1100 two."""
+    import ctypes
+
+    class Consts(ctypes.Structure):
+        _fields_ = [("length", ctypes.c_float * 3), ("sin", ctypes.c_double * 3), ("cos", ctypes.c_double * 3)]
+
+    lib = _abi_fused()
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    c = Consts((ctypes.c_float * 3)(*BOND_LENGTHS), (ctypes.c_double * 3)(*(math.sin(a) for a in BOND_ANGLES)),
+               (ctypes.c_double * 3)(*(math.cos(a) for a in BOND_ANGLES)))
+    B = 7
+    gen = torch.Generator(device=device).manual_seed(N + shift)
+    raw = torch.randn(B, 2 * (N - 3), generator=gen, device=device).to(dtype)
+
+    def view(shape, dt, fill):
+        n = math.prod(shape)
+        buf = torch.full((n + 8,), fill, dtype=dt, device=device)
+        return buf[shift : shift + n].view(shape)
+
+    raw_h = view(raw.shape, dtype, 0.0)
+    raw_h.copy_(raw)
+    xyz_h = view((B, N, 3), dtype, float("nan"))
+    xyz_f = torch.full((B, N, 3), float("nan"), device=device)
+    raw_f = raw.float()
+    assert lib.cufk_torsion_fwd(_CODES[dtype], p(raw_h), raw_h.stride(0), ctypes.byref(c), p(xyz_h), B, N, st) == 0
+    assert lib.cufk_torsion_fwd(0, p(raw_f), raw_f.stride(0), ctypes.byref(c), p(xyz_f), B, N, st) == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(xyz_f).all()
+    assert torch.equal(xyz_h, xyz_f.to(dtype))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
 @pytest.mark.parametrize("N", [300, 771])
 def test_torsion_loss_forward_stores_the_torsion_forwards_positions(device, dtype, N):
